@@ -1,0 +1,140 @@
+/*
+ * q4kv.h -- C ABI of the MI355X QSA KV-cache library (libq4kv.so).
+ *
+ * Drop-in for SuzuQu-Engine's KV-cache hot path: every function below keeps
+ * the name, signature, argument meaning and error convention of the
+ * reference declaration it cites (upstream src/q4.h). All functions return
+ * false (or NULL) on bad arguments or a launch error, print "q4 hip: ..." to
+ * stderr for launch errors, and never abort. Device work is enqueued on one
+ * library stream and is asynchronous unless stated otherwise.
+ *
+ * Cache layout (unchanged from the reference, src/q4_fwd.c:644-655): one K
+ * and one V buffer per QSA layer, token-major [pos][kv_head][head_dim] with
+ * bytes-per-token bpt = n_kvh*hd*4 (f32), n_kvh*hd*2 (f16) or
+ * n_kvh*(hd/32)*34 (q8_0, blocks of {fp16 scale, 32 x int8}).
+ * KV width codes ("kind", "kv_f16"): 0 = f32, 1 = f16, 2 = q8_0.
+ */
+#ifndef Q4KV_H
+#define Q4KV_H
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { Q4KV_F32 = 0, Q4KV_F16 = 1, Q4KV_Q8 = 2 };
+
+/* ---------------- runtime (src/q4.h:708-710, 877-880, 948-949) ---------- */
+bool q4_hip_init(void);                       /* src/q4.h:708 */
+void q4_hip_shutdown(void);                   /* src/q4.h:709 */
+bool q4_hip_ok(void);                         /* src/q4.h:710 */
+void *q4_hip_malloc(size_t n);                /* src/q4.h:877 */
+void q4_hip_free(void *p);                    /* src/q4.h:878 */
+bool q4_hip_h2d(void *d, const void *h, size_t n); /* src/q4.h:879, synchronous */
+bool q4_hip_d2h(void *h, const void *d, size_t n); /* src/q4.h:880, synchronous */
+void q4_hip_sync(void);                       /* src/q4.h:948 */
+void q4_hip_clear(void);                      /* src/q4.h:949 */
+bool q4_hip_d2h_async(void *h, const void *d, uint64_t n); /* src/q4.h:787 */
+bool q4_hip_h2d_async(void *d, const void *h, uint64_t n); /* src/q4.h:788 */
+bool q4_hip_stream_sync(void);                /* src/q4.h:789 */
+/* f32 KV width store, n floats device-to-device (src/q4.h:851). Stream
+ * ordered; the reference's version also waits for completion. */
+bool q4_hip_copy(float *d, const float *s, uint64_t n);
+
+/* Graph capture of the compute stream (src/q4.h:782-786). */
+int q4_hip_graph_begin(void);
+void *q4_hip_graph_end(void);
+uint32_t q4_hip_graph_nodes(void *exec);
+bool q4_hip_graph_launch(void *exec);
+void q4_hip_graph_free(void *exec);
+
+/* Device decode position for graph-captured kernels (src/q4.h:686-688). */
+void q4_hip_pos_push(int32_t pos);
+int q4_hip_capturing(void);
+int q4_hip_pos_dev_ok(void);
+
+/* ---------------- KV writes (a1-a3) ---------------- */
+/* fp32 [n] -> q8_0 blocks, n % 32 == 0 (src/q4.h:929). */
+bool q4_hip_f32_to_q8(void *dst_q8, const float *src, uint64_t n);
+/* fp32 [n] -> fp16 [n], round-to-nearest-even (src/q4.h:928). */
+bool q4_hip_f32_to_f16(void *dst_f16, const float *src, uint64_t n);
+/* Append one token's K and V (n floats each) at the device position into
+ * caches with bpt bytes per token, width `kind` (src/q4.h:694-695). */
+bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k, const float *v,
+                        uint32_t n, uint32_t bpt, int kind);
+
+/* ---------------- QSA attention (a5-a9) ---------------- */
+/* Dense causal attention: token t of n_tok attends positions
+ * 0 .. min(kv_base+t+1, max_kv)-1. q/gate/out are [n_tok][n_head][hd] fp32;
+ * out = softmax(q.k*scale) @ v * sigmoid(gate) (src/q4.h:906-909). */
+bool q4_hip_qsa_decode_n(const float *d_q, const void *d_kcache, const void *d_vcache,
+                         const float *d_gate, float *d_out, uint32_t n_head,
+                         uint32_t n_kvh, uint32_t hd, uint32_t n_tok, uint32_t kv_base,
+                         uint32_t max_kv, float scale, int kv_f16);
+/* Attention over an explicit position list: row t is idx[t*width + j],
+ * -1 = padding, shared by all KV heads (src/q4.h:911-915). */
+bool q4_hip_qsa_decode_idx(const float *d_q, const void *d_kcache, const void *d_vcache,
+                           const float *d_gate, float *d_out, const int32_t *idx,
+                           uint32_t width, uint32_t n_head, uint32_t n_kvh, uint32_t hd,
+                           uint32_t n_tok, uint32_t max_kv, float scale, int kv_f16);
+/* One-token dense decode over n_kv positions (src/q4.h:621-624). */
+bool q4_hip_qsa_decode(const float *d_q, const void *d_kcache, const void *d_vcache,
+                       const float *d_gate, float *d_out, uint32_t n_head, uint32_t n_kvh,
+                       uint32_t hd, uint32_t n_kv, uint32_t max_kv, float scale, int kv_f16);
+/* Internal scratch for split decode (src/q4.h:704). The library allocates
+ * its split-KV partial buffer in q4_hip_init; this only reports it. */
+bool q4_hip_qsa_topk_alloc(void);
+
+/* ---------------- extensions (no reference counterpart) ----------------
+ * Additive entry points; nothing above depends on them. */
+
+/* q4_hip_qsa_decode_idx with a separate position list per KV head: the list
+ * of (token t, kv head kh) starts at idx + t*tok_stride + kh*kvh_stride.
+ * With tok_stride = width and kvh_stride = 0 it is q4_hip_qsa_decode_idx.
+ * d_gate may be NULL (no gate). */
+bool q4_hip_qsa_decode_idx_kv(const float *d_q, const void *d_kcache, const void *d_vcache,
+                              const float *d_gate, float *d_out, const int32_t *idx,
+                              uint32_t width, uint64_t tok_stride, uint64_t kvh_stride,
+                              uint32_t n_head, uint32_t n_kvh, uint32_t hd, uint32_t n_tok,
+                              uint32_t max_kv, float scale, int kv_f16);
+
+/* One decode item of a batched launch: an independent sequence (or layer)
+ * with its own caches, query, output and per-KV-head position lists.
+ * All pointers are device pointers; the descriptor array itself lives in
+ * device memory (caller-owned, 64 bytes per entry). */
+typedef struct {
+    const void *kcache;     /* [max_kv][n_kvh][row] */
+    const void *vcache;
+    const float *q;         /* [n_head][hd] */
+    const float *gate;      /* [n_head][hd] or NULL */
+    float *out;             /* [n_head][hd] */
+    const int32_t *idx;     /* list of kv head kh at idx + kh*idx_kvh_stride; NULL = dense */
+    uint32_t n_sel;         /* list length (indexed) or visible positions (dense) */
+    uint32_t idx_kvh_stride;
+    uint32_t max_kv;
+    uint32_t reserved;
+} q4kv_seq_desc;
+
+/* Decode one token for each of n_seq independent items in one launch
+ * (batched serving, or several layers' caches with queries already known).
+ * max_n bounds the descriptors' n_sel; it sizes the split-KV work division
+ * only (a larger n_sel is still processed in full). */
+bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n_seq,
+                             uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
+                             int kv_f16, uint32_t max_n);
+
+/* Pinned host buffers for restoring a session KV image (hipHostMalloc). */
+void *q4_hip_host_alloc(size_t n);
+void q4_hip_host_free(void *p);
+
+/* Event timing on the library stream (benchmark support). */
+bool q4kv_timer_begin(int slot);
+double q4kv_timer_end_ms(int slot);
+int q4kv_device_info(char *name, int name_len, int *n_cu, int *clock_khz);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,168 @@
+/*
+ * q4kv_quant.hip -- KV-cache write kernels: fp32 -> q8_0 / fp16 / fp32 rows.
+ *
+ * q8_0 block format (src/q4_rocm.cu:7221-7238): 32 values per block, 34 bytes:
+ * a little-endian fp16 scale d = fp16(amax / 127) followed by 32 int8
+ * q = clamp(rint(x * (1/d)), -127, 127). The arithmetic here is IEEE
+ * binary32 with round-to-nearest-even everywhere (explicitly rounded divide,
+ * no contraction), so the bytes equal the source semantics of the reference
+ * kernel bit for bit.
+ *
+ * Layout on gfx950: 8 lanes cooperate on one block (one float4 each, so a
+ * wave reads 1 KiB of contiguous input), the block's absolute max is reduced
+ * across the 8 lanes, and a workgroup's 32 output blocks (1088 bytes) are
+ * assembled in LDS and written back as 68 coalesced 16-byte stores.
+ */
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include "q4kv_internal.h"
+
+extern "C" {
+#include "q4kv.h"
+}
+
+#define QBLK_PER_WG 32u /* 256 threads / 8 lanes per block */
+
+/* Quantise blocks [blk0, blk0+32) of src into dst (block-indexed). */
+__device__ static void q8_quant_wg(const float *__restrict__ src, uint8_t *__restrict__ dst,
+                                   uint64_t nblocks, uint64_t blk0, bool src_al16,
+                                   bool dst_al16) {
+    __shared__ __attribute__((aligned(16))) uint8_t ob[QBLK_PER_WG * 34u];
+    const uint32_t t = threadIdx.x, lb = t >> 3, part = t & 7u;
+    const uint64_t b = blk0 + lb;
+    const bool live = b < nblocks;
+    float x0 = 0.f, x1 = 0.f, x2 = 0.f, x3 = 0.f;
+    if (live) {
+        const float *p = src + b * 32u + part * 4u;
+        if (src_al16) {
+            float4 v = *(const float4 *)p;
+            x0 = v.x; x1 = v.y; x2 = v.z; x3 = v.w;
+        } else {
+            x0 = p[0]; x1 = p[1]; x2 = p[2]; x3 = p[3];
+        }
+    }
+    float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
+    a = fmaxf(a, __shfl_xor(a, 1, 8));
+    a = fmaxf(a, __shfl_xor(a, 2, 8));
+    a = fmaxf(a, __shfl_xor(a, 4, 8));
+    const float d = __fdiv_rn(a, 127.f);
+    const float id = d > 0.f ? __fdiv_rn(1.f, d) : 0.f;
+    int q[4];
+    const float xs[4] = {x0, x1, x2, x3};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int v = (int)__builtin_rintf(__fmul_rn(xs[i], id));
+        v = v > 127 ? 127 : v;
+        v = v < -127 ? -127 : v;
+        q[i] = v;
+    }
+    uint8_t *o = ob + lb * 34u;
+    /* The block's int8 payload starts 2 bytes in, so 16-bit LDS stores. */
+    *(uint16_t *)(o + 2u + part * 4u) = (uint16_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8));
+    *(uint16_t *)(o + 4u + part * 4u) = (uint16_t)((q[2] & 0xff) | ((q[3] & 0xff) << 8));
+    if (part == 0) *(uint16_t *)o = __half_as_ushort(__float2half_rn(d));
+    __syncthreads();
+    const uint64_t nb = nblocks - blk0 < QBLK_PER_WG ? nblocks - blk0 : QBLK_PER_WG;
+    uint8_t *out = dst + blk0 * 34u;
+    if (dst_al16 && nb == QBLK_PER_WG) {
+        if (t < QBLK_PER_WG * 34u / 16u) ((uint4 *)out)[t] = ((const uint4 *)ob)[t];
+    } else {
+        for (uint32_t i = t; i < nb * 34u; i += blockDim.x) out[i] = ob[i];
+    }
+}
+
+__global__ __launch_bounds__(256) static void f32_to_q8_k(const float *__restrict__ src,
+                                                          uint8_t *__restrict__ dst,
+                                                          uint64_t nblocks, int src_al16,
+                                                          int dst_al16) {
+    q8_quant_wg(src, dst, nblocks, (uint64_t)blockIdx.x * QBLK_PER_WG, src_al16 != 0,
+                dst_al16 != 0);
+}
+
+/* fp16 width: RNE per element (src/q4_rocm.cu:7208-7211), 4 per thread. */
+__global__ __launch_bounds__(256) static void f32_to_f16_k(const float *__restrict__ src,
+                                                           __half *__restrict__ dst,
+                                                           uint64_t n, int vec) {
+    const uint64_t i4 = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4u;
+    if (i4 >= n) return;
+    if (vec && i4 + 4u <= n) {
+        float4 v = *(const float4 *)(src + i4);
+        uint2 o;
+        o.x = (uint32_t)__half_as_ushort(__float2half_rn(v.x)) |
+              ((uint32_t)__half_as_ushort(__float2half_rn(v.y)) << 16);
+        o.y = (uint32_t)__half_as_ushort(__float2half_rn(v.z)) |
+              ((uint32_t)__half_as_ushort(__float2half_rn(v.w)) << 16);
+        *(uint2 *)(dst + i4) = o;
+    } else {
+        for (uint64_t i = i4; i < n && i < i4 + 4u; i++) dst[i] = __float2half_rn(src[i]);
+    }
+}
+
+/* Device-position append of one token's K and V rows (n floats each) into
+ * caches with bpt bytes per token (src/q4_rocm.cu:7962-8012). grid.y = 0
+ * writes K, 1 writes V. The position is read from device memory so the
+ * launch can sit in a captured graph and replay for every token. */
+__global__ __launch_bounds__(256) static void kv_append_k(const float *__restrict__ k,
+                                                          const float *__restrict__ v,
+                                                          uint8_t *kc, uint8_t *vc, uint32_t n,
+                                                          uint32_t bpt, int kind,
+                                                          const int32_t *__restrict__ pp) {
+    const size_t off = (size_t)(uint32_t)*pp * bpt;
+    const float *src = blockIdx.y ? v : k;
+    uint8_t *dst = (blockIdx.y ? vc : kc) + off;
+    if (kind == Q4KV_Q8) {
+        const bool s_al = ((uintptr_t)src & 15u) == 0;
+        const bool d_al = ((uintptr_t)dst & 15u) == 0;
+        q8_quant_wg(src, dst, n / 32u, (uint64_t)blockIdx.x * QBLK_PER_WG, s_al, d_al);
+    } else {
+        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n;
+             i += gridDim.x * blockDim.x) {
+            if (kind == Q4KV_F16)
+                ((__half *)dst)[i] = __float2half_rn(src[i]);
+            else
+                ((float *)dst)[i] = src[i];
+        }
+    }
+}
+
+extern "C" bool q4_hip_f32_to_q8(void *dst_q8, const float *src, uint64_t n) {
+    if (!q4kv_ok || !dst_q8 || !src || n == 0 || (n % 32u) != 0) return false;
+    (void)hipGetLastError();
+    const uint64_t nb = n / 32u;
+    const uint64_t grid = (nb + QBLK_PER_WG - 1) / QBLK_PER_WG;
+    if (grid > 0x7fffffffull) return false;
+    f32_to_q8_k<<<(uint32_t)grid, 256, 0, q4kv_stream>>>(
+        src, (uint8_t *)dst_q8, nb, ((uintptr_t)src & 15u) == 0,
+        ((uintptr_t)dst_q8 & 15u) == 0);
+    return q4kv_launch_ok("f32_to_q8");
+}
+
+extern "C" bool q4_hip_f32_to_f16(void *dst_f16, const float *src, uint64_t n) {
+    if (!q4kv_ok || !dst_f16 || !src || !n) return false;
+    (void)hipGetLastError();
+    const uint64_t threads = (n + 3u) / 4u;
+    const uint64_t grid = (threads + 255u) / 256u;
+    if (grid > 0x7fffffffull) return false;
+    const int vec = ((uintptr_t)src & 15u) == 0 && ((uintptr_t)dst_f16 & 7u) == 0;
+    f32_to_f16_k<<<(uint32_t)grid, 256, 0, q4kv_stream>>>(src, (__half *)dst_f16, n, vec);
+    return q4kv_launch_ok("f32_to_f16");
+}
+
+extern "C" bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k,
+                                   const float *v, uint32_t n, uint32_t bpt, int kind) {
+    if (!q4kv_ok || !q4kv_pos_d || !kcache || !vcache || !k || !v || !n || !bpt)
+        return false;
+    if (kind < Q4KV_F32 || kind > Q4KV_Q8) return false;
+    if (kind == Q4KV_Q8 && (n % 32u)) return false;
+    (void)hipGetLastError();
+    uint32_t gx;
+    if (kind == Q4KV_Q8)
+        gx = (n / 32u + QBLK_PER_WG - 1) / QBLK_PER_WG;
+    else
+        gx = (n + 255u) / 256u;
+    dim3 grid(gx, 2);
+    kv_append_k<<<grid, 256, 0, q4kv_stream>>>(k, v, (uint8_t *)kcache, (uint8_t *)vcache, n,
+                                               bpt, kind, q4kv_pos_d);
+    return q4kv_launch_ok("kv_append");
+}
