@@ -1,0 +1,314 @@
+#!/usr/bin/env python3
+"""QSA KV-cache hot path benchmark on one MI355X.
+
+Workload ("step" = one decode token through the KV path of the 12 QSA
+layers): each layer owns a 262144-token q8_0 K and V cache (2 KV heads x
+256 dims, 272-byte rows); the step appends the new token's K/V rows (q8_0
+quantise at its position) and runs sparse attention for 16 query heads over
+a per-KV-head selection of 2051 sorted positions (3 sinks + 512 recent +
+1536 uniform). Inputs are synthetic (device-generated N(0,1) with 4 outlier
+channels x8), resident in HBM before timing. 16 selection sets with
+different decode positions rotate across steps so the 27 MB a step gathers
+is not served from the 256 MB Infinity Cache.
+
+Modes:
+  batched    -- all 12 layers' appends in one launch, their attention in one
+                split-KV launch + merge (headline `value`).
+  sequential -- per layer append + attention launches, captured into one
+                hipGraph per step (what a batch-1 decode executes).
+
+Prints one JSON line (see the metric contract in DESIGN.md).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "suzuqu-engine-4exp_amd"
+for _p in (PKG, ROOT / "tests"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import q4kv  # noqa: E402
+
+METRIC = "QSA decode µs/layer + achieved HBM GB/s (% of peak) at 262K q8_0 ctx, 1 GPU"
+PEAK_GBS = 8000.0
+CTX, N_KVH, HD, N_HEAD, WIDTH = 262144, 2, 256, 16, 2051
+OUTLIERS = (3, 77, 150, 201)
+ROW = HD // 32 * 34                       # 272 B per (position, kv head)
+BPT = N_KVH * ROW                         # 544 B per token
+GATHER_B = 2 * N_KVH * WIDTH * ROW        # K+V rows gathered per layer
+IDX_B = N_KVH * WIDTH * 4
+QO_B = N_HEAD * HD * 4
+APPEND_B = 2 * N_KVH * HD * 4 + 2 * BPT   # read fp32 K,V rows + write q8 rows
+LAYER_B = GATHER_B + IDX_B + 2 * QO_B + APPEND_B  # 2 285 848 B
+SPLIT_KERNEL_B = GATHER_B + IDX_B + QO_B  # what the split-KV kernel must read
+
+
+def selection(rng, pos):
+    n_uni = WIDTH - 3 - 512
+    uni = rng.choice(pos - 512 - 2, size=n_uni, replace=False).astype(np.int64) + 3
+    return np.concatenate([np.arange(3), np.sort(uni),
+                           np.arange(pos - 511, pos + 1)]).astype(np.int32)
+
+
+class Bench:
+    def __init__(self, layers: int, sets: int):
+        self.L, self.R = layers, sets
+        self.rt = rt = q4kv.Runtime()
+        self.lib = lib = rt.lib
+        synth = C.CDLL(str(PKG / "lib" / "libq4kv_synth.so"))
+        synth.q4kv_synth_heads.restype = C.c_int
+        synth.q4kv_synth_heads.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint64,
+                                           C.c_int, C.c_int, C.c_int, C.c_int]
+
+        def gen(ptr, n, seed):
+            assert synth.q4kv_synth_heads(ptr, n, HD, seed, *OUTLIERS) == 0
+
+        self.gen = gen
+        n = CTX * N_KVH * HD
+        scratch = rt.alloc(n * 4)
+        self.kc, self.vc = [], []
+        for layer in range(self.L):
+            for lst, seed in ((self.kc, 2 * layer + 1), (self.vc, 2 * layer + 2)):
+                cache = rt.alloc(CTX * BPT)
+                gen(scratch, n, 1000 + seed)
+                assert lib.q4_hip_f32_to_q8(cache, scratch, n)
+                lst.append(cache)
+        rt.sync()
+        rt.free(scratch)
+        # per-set decode positions, selections and fresh q / new K,V rows
+        self.pos = [CTX - 1 - 600 * s for s in range(self.R)]
+        rng = np.random.default_rng(1235)
+        sel = np.empty((self.R, self.L, N_KVH, WIDTH), np.int32)
+        for s in range(self.R):
+            for layer in range(self.L):
+                for kh in range(N_KVH):
+                    sel[s, layer, kh] = selection(rng, self.pos[s])
+        self.sel_host = sel
+        self.d_sel = rt.upload(sel)
+        self.d_q = rt.alloc(self.R * self.L * N_HEAD * HD * 4)
+        self.d_nk = rt.alloc(self.R * self.L * N_KVH * HD * 4)
+        self.d_nv = rt.alloc(self.R * self.L * N_KVH * HD * 4)
+        gen(self.d_q, self.R * self.L * N_HEAD * HD, 77)
+        gen(self.d_nk, self.R * self.L * N_KVH * HD, 78)
+        gen(self.d_nv, self.R * self.L * N_KVH * HD, 79)
+        self.d_out = rt.alloc(self.L * N_HEAD * HD * 4)
+        seq = (q4kv.SeqDesc * (self.R * self.L))()
+        app = (q4kv.AppendDesc * (self.R * self.L))()
+        for s in range(self.R):
+            for layer in range(self.L):
+                i = s * self.L + layer
+                seq[i] = q4kv.SeqDesc(self.kc[layer], self.vc[layer], self.q_ptr(s, layer),
+                                      None, self.d_out + layer * QO_B,
+                                      self.sel_ptr(s, layer), WIDTH, WIDTH, CTX, 0)
+                app[i] = q4kv.AppendDesc(self.kc[layer], self.vc[layer],
+                                         self.row_ptr(self.d_nk, s, layer),
+                                         self.row_ptr(self.d_nv, s, layer), self.pos[s], 0)
+        self.d_seq = rt.alloc(C.sizeof(seq))
+        self.d_app = rt.alloc(C.sizeof(app))
+        assert lib.q4_hip_h2d(self.d_seq, C.addressof(seq), C.sizeof(seq))
+        assert lib.q4_hip_h2d(self.d_app, C.addressof(app), C.sizeof(app))
+        self.graphs = None
+
+    def q_ptr(self, s, layer):
+        return self.d_q + (s * self.L + layer) * QO_B
+
+    def sel_ptr(self, s, layer):
+        return self.d_sel + (s * self.L + layer) * IDX_B
+
+    def row_ptr(self, base, s, layer):
+        return base + (s * self.L + layer) * N_KVH * HD * 4
+
+    # ---- one step -----------------------------------------------------------
+    def step_batched(self, s):
+        lib = self.lib
+        ok = lib.q4_hip_kv_append_batch(self.d_app + s * self.L * C.sizeof(q4kv.AppendDesc),
+                                        self.L, N_KVH * HD, BPT, q4kv.KV_Q8)
+        ok = ok and lib.q4_hip_qsa_decode_batch(self.d_seq + s * self.L * 64, self.L, N_HEAD,
+                                                N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH)
+        assert ok
+
+    def _enqueue_sequential(self, s):
+        lib = self.lib
+        ok = True
+        for layer in range(self.L):
+            ok = ok and lib.q4_hip_kv_append_d(self.kc[layer], self.vc[layer],
+                                               self.row_ptr(self.d_nk, s, layer),
+                                               self.row_ptr(self.d_nv, s, layer),
+                                               N_KVH * HD, BPT, q4kv.KV_Q8)
+            ok = ok and lib.q4_hip_qsa_decode_idx_kv(
+                self.q_ptr(s, layer), self.kc[layer], self.vc[layer], None,
+                self.d_out + layer * QO_B, self.sel_ptr(s, layer), WIDTH, N_KVH * WIDTH,
+                WIDTH, N_HEAD, N_KVH, HD, 1, CTX, 1.0 / 16, q4kv.KV_Q8)
+        return ok
+
+    def step_sequential(self, s):
+        if self.graphs is None:
+            self.graphs = []
+            for r in range(self.R):
+                assert self.lib.q4_hip_graph_begin() == 1
+                ok = self._enqueue_sequential(r)
+                g = self.lib.q4_hip_graph_end()
+                assert ok and g, "graph capture failed"
+                self.graphs.append(g)
+        self.lib.q4_hip_pos_push(self.pos[s])
+        assert self.lib.q4_hip_graph_launch(self.graphs[s])
+
+    def timed(self, step, steps, warmup, prof=False):
+        for i in range(warmup):
+            step(i % self.R)
+        self.rt.sync()
+        if prof:
+            assert self.lib.q4kv_prof_begin(min(steps, 4096))
+        assert self.lib.q4kv_timer_begin(0)
+        t0 = time.perf_counter()
+        for i in range(steps):
+            step(i % self.R)
+        self.rt.sync()
+        wall = time.perf_counter() - t0
+        gpu_ms = self.lib.q4kv_timer_end_ms(0)
+        kern = None
+        if prof:
+            tot = C.c_double()
+            n = self.lib.q4kv_prof_end(C.byref(tot))
+            kern = tot.value / n if n > 0 else None
+        return wall, gpu_ms / 1e3, kern
+
+    # ---- parity of the last batched step vs the oracle (layer 0) ------------
+    def check_and_cpu(self, cpu_seconds, threads):
+        from oracle_ffi import Oracle
+        from synth import assert_attn_close
+
+        orc = Oracle()
+        rt, s, layer = self.rt, 0, 0
+        self.rt.sync()
+        kb = rt.download(self.kc[layer], CTX * BPT)
+        vb = rt.download(self.vc[layer], CTX * BPT)
+        q = rt.download(self.q_ptr(s, layer), QO_B, np.float32).reshape(1, N_HEAD, HD)
+        nk = rt.download(self.row_ptr(self.d_nk, s, layer), N_KVH * HD * 4, np.float32)
+        nv = rt.download(self.row_ptr(self.d_nv, s, layer), N_KVH * HD * 4, np.float32)
+        self.step_batched(s)
+        rt.sync()
+        got = rt.download(self.d_out + layer * QO_B, QO_B, np.float32).reshape(1, N_HEAD, HD)
+        # the downloaded caches already hold set 0's appended row: re-append on
+        # the host copy, and check those bytes against the oracle's quantiser
+        hk, hv = kb.copy(), vb.copy()
+        pos = self.pos[s]
+        orc.lib.orc_kv_append(hk.ctypes.data, hv.ctypes.data, nk.ctypes.data, nv.ctypes.data,
+                              N_KVH * HD, BPT, 2, pos)
+        rows_ok = bool(np.array_equal(hk[pos * BPT:(pos + 1) * BPT], kb[pos * BPT:(pos + 1) * BPT])
+                       and np.array_equal(hv[pos * BPT:(pos + 1) * BPT],
+                                          vb[pos * BPT:(pos + 1) * BPT]))
+        sel = self.sel_host[s, layer].ravel()
+        kw = dict(idx=sel, width=WIDTH, tok_stride=N_KVH * WIDTH, kvh_stride=WIDTH, max_kv=CTX)
+        want = orc.attn(q, hk, hv, 2, N_HEAD, N_KVH, HD, 1, **kw)
+        err = assert_attn_close(got, want, what="bench parity")
+        res = {"parity_max_abs_err": err, "append_rows_bit_exact": rows_ok}
+        if cpu_seconds <= 0:
+            return res, None
+
+        def run(nthreads, budget):
+            n, t0 = 0, time.perf_counter()
+            while True:
+                orc.lib.orc_kv_append(hk.ctypes.data, hv.ctypes.data, nk.ctypes.data,
+                                      nv.ctypes.data, N_KVH * HD, BPT, 2, pos)
+                orc.attn(q, hk, hv, 2, N_HEAD, N_KVH, HD, 1, dbl=False, threads=nthreads, **kw)
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= budget:
+                    return n, el
+
+        n1, el1 = run(1, cpu_seconds)
+        nt, elt = run(threads, max(2.0, cpu_seconds / 3))
+        cpu = {
+            "value": round(n1 * LAYER_B / el1 / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": (f"{n1} single-layer decode steps (q8_0 append + sparse attention of "
+                       f"16 heads over 2x2051 rows of one 262144-token q8_0 layer cache), "
+                       f"fp32 C restatement of src/q4_fwd.c:330-407, 1 thread, {el1:.1f} s"),
+            "us_per_layer": round(el1 / n1 * 1e6, 1),
+            "openmp": {"threads": threads, "value": round(nt * LAYER_B / elt / 1e9, 4),
+                       "us_per_layer": round(elt / nt * 1e6, 1)},
+            "host_cpu": _cpu_model(),
+        }
+        return res, cpu
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--sets", type=int, default=16)
+    ap.add_argument("--mode", choices=["batched", "sequential", "both"], default="both")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the QSA KV path runs on a single MI355X "
+              "(no collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    b = Bench(args.layers, args.sets)
+    res = {}
+    if args.mode in ("batched", "both"):
+        res["batched"] = b.timed(b.step_batched, args.steps, args.warmup, prof=True)
+    if args.mode in ("sequential", "both"):
+        res["sequential"] = b.timed(b.step_sequential, args.steps, args.warmup)
+    threads = min(16, os.cpu_count() or 1)
+    parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
+    head = "batched" if "batched" in res else "sequential"
+    wall, gpu_s, kern_s = res[head]
+    K, L = args.steps, args.layers
+    value = K * L * LAYER_B / wall / 1e9
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(wall / K * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (device-generated N(0,1), 4 outlier channels x8 per head)",
+        "config": {
+            "workload": (f"config1 QSA sparse decode: {L} QSA layers x (q8_0 append + sparse "
+                         f"attention), {CTX}-token q8_0 cache per layer, 16 Q / 2 KV heads, "
+                         f"hd 256, 2051 selected positions per KV head, {head} launch"),
+            "kv": "q8_0", "ctx": CTX, "layers_per_step": L, "selection_sets": args.sets,
+            "bytes_per_layer": LAYER_B, "parallelism": "single GPU",
+        },
+        "us_per_layer": round(wall / (K * L) * 1e6, 4),
+        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+    }
+    for mode, (w, g, _) in res.items():
+        out[f"{mode}_us_per_layer"] = round(w / (K * L) * 1e6, 4)
+        out[f"{mode}_gbs"] = round(K * L * LAYER_B / w / 1e9, 2)
+        out[f"{mode}_gpu_event_us_per_layer"] = round(g / (K * L) * 1e6, 4)
+    if kern_s:
+        ach = L * SPLIT_KERNEL_B / (kern_s / 1e3) / 1e9
+        out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS,
+                           "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4), "traffic": None,
+                           "kernel": "qsa_attn_k<q8,batch>",
+                           "kernel_us": round(kern_s * 1e3, 3),
+                           "bytes_per_launch": L * SPLIT_KERNEL_B}
+    out.update(parity)
+    out["cpu_baseline"] = cpu
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

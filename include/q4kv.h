@@ -125,6 +125,19 @@ bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n_seq,
                              uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
                              int kv_f16, uint32_t max_n);
 
+/* One token's K/V rows for one cache, for a batched append. */
+typedef struct {
+    void *kcache, *vcache; /* cache bases (token 0) */
+    const float *k, *v;    /* n fp32 each */
+    uint32_t pos;          /* token position to write */
+    uint32_t reserved;
+} q4kv_append_desc;
+
+/* Append into n_desc caches in one launch (the per-layer
+ * q4_hip_kv_append_d of a decode step, batched). */
+bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc, uint32_t n,
+                            uint32_t bpt, int kind);
+
 /* Pinned host buffers for restoring a session KV image (hipHostMalloc). */
 void *q4_hip_host_alloc(size_t n);
 void q4_hip_host_free(void *p);
@@ -133,6 +146,11 @@ void q4_hip_host_free(void *p);
 bool q4kv_timer_begin(int slot);
 double q4kv_timer_end_ms(int slot);
 int q4kv_device_info(char *name, int name_len, int *n_cu, int *clock_khz);
+/* Arm per-launch event timing of the split-KV attention kernel for up to
+ * max_launches launches; q4kv_prof_end waits and returns the number timed
+ * and their summed duration in ms. */
+bool q4kv_prof_begin(int max_launches);
+int q4kv_prof_end(double *total_ms);
 
 #ifdef __cplusplus
 }

@@ -74,14 +74,17 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
     Item it;
     if (MODE == MODE_BATCH) {
         const q4kv_seq_desc *d = a.seqs + t;
-        it.kc = (const uint8_t *)d->kcache;
-        it.vc = (const uint8_t *)d->vcache;
-        it.q = d->q + hoff;
-        it.gate = d->gate ? d->gate + hoff : nullptr;
-        it.out = d->out + hoff;
-        it.max_kv = d->max_kv;
-        it.list = d->idx ? d->idx + (size_t)kh * d->idx_kvh_stride : nullptr;
-        it.n = d->idx ? d->n_sel : (d->n_sel < d->max_kv ? d->n_sel : d->max_kv);
+        const float *gate = ldg(&d->gate);
+        const int32_t *idx = ldg(&d->idx);
+        const uint32_t n_sel = ldg(&d->n_sel);
+        it.kc = (const uint8_t *)ldg(&d->kcache);
+        it.vc = (const uint8_t *)ldg(&d->vcache);
+        it.q = ldg(&d->q) + hoff;
+        it.gate = gate ? gate + hoff : nullptr;
+        it.out = ldg(&d->out) + hoff;
+        it.max_kv = ldg(&d->max_kv);
+        it.list = idx ? idx + (size_t)kh * ldg(&d->idx_kvh_stride) : nullptr;
+        it.n = idx ? n_sel : (n_sel < it.max_kv ? n_sel : it.max_kv);
     } else {
         const size_t qo = (size_t)t * a.n_head * a.hd + hoff;
         it.kc = a.kc;
@@ -173,24 +176,120 @@ __device__ static inline _Float16 split_hl(float x, bool lo) {
     return lo ? (_Float16)(x - (float)h) : h;
 }
 
+#ifdef Q4KV_TRACE
+/* Debug-only phase timestamps (100 MHz wall clock) of thread 0 of every
+ * workgroup: [block][slot]. Not compiled into the product library. */
+__device__ uint64_t q4kv_trace_buf[4096 * 16];
+#define TRACE(slot)                                                                \
+    do {                                                                           \
+        if (threadIdx.x == 0)                                                      \
+            q4kv_trace_buf[((blockIdx.y * gridDim.x + blockIdx.x) & 4095u) * 16u + (slot)] = \
+                wall_clock64();                                                    \
+    } while (0)
+#else
+#define TRACE(slot) do { } while (0)
+#endif
+
 template <int KIND> struct KCfg;
 template <> struct KCfg<Q4KV_Q8> { static constexpr uint32_t CP = 64, RMAX = 272; };
 template <> struct KCfg<Q4KV_F16> { static constexpr uint32_t CP = 64, RMAX = 512; };
 template <> struct KCfg<Q4KV_F32> { static constexpr uint32_t CP = 32, RMAX = 1024; };
 
+typedef float fv2 __attribute__((ext_vector_type(2)));
+
+/* Position of list entry j of an item, or -1 (padding, beyond the list, or
+ * outside the cache). */
+__device__ static inline int32_t item_pos(const Item &it, uint32_t j) {
+    if (j >= it.n) return -1;
+    int32_t p = it.list ? ldg(it.list + j) : (int32_t)j;
+    return (p < 0 || (uint32_t)p >= it.max_kv) ? -1 : p;
+}
+
+/* Positions of list entries j[0..N), in two steps so that the index loads
+ * (issued back to back, one memory round trip) are only waited for where
+ * the positions are used: pos_issue loads the raw entries, pos_finish
+ * maps them to positions (-1 for padding / out of range). Requires n > 0. */
+template <int N, int MODE>
+__device__ static inline void pos_issue(const Item &it, const uint32_t (&j)[N],
+                                        int32_t (&raw)[N]) {
+    if (MODE == MODE_DENSE) {
+#pragma unroll
+        for (int u = 0; u < N; u++) raw[u] = (int32_t)j[u];
+    } else {
+        /* no branch on the list pointer (a branch would force a wait at its
+         * merge): dense batch items load a harmless word and keep j */
+        const bool has = MODE == MODE_INDEXED || it.list != nullptr;
+#pragma unroll
+        for (int u = 0; u < N; u++) {
+            const int32_t *src = has ? it.list + (j[u] < it.n ? j[u] : it.n - 1u)
+                                     : (const int32_t *)it.q;
+            raw[u] = *(const GLOBAL int32_t *)src;
+        }
+    }
+}
+template <int N, int MODE>
+__device__ static inline void pos_finish(const Item &it, const uint32_t (&j)[N],
+                                         const int32_t (&raw)[N], int32_t (&p)[N]) {
+    const bool has = MODE == MODE_INDEXED || (MODE == MODE_BATCH && it.list != nullptr);
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+        const int32_t r = has ? raw[u] : (int32_t)j[u];
+        p[u] = (j[u] < it.n && r >= 0 && (uint32_t)r < it.max_kv) ? r : -1;
+    }
+}
+
+/* 16 bytes global -> LDS without passing through VGPRs (gfx950
+ * global_load_lds_dwordx4). Every active lane of the wave writes its 16 bytes
+ * at lds_wave_base + 16*lane. */
+__device__ static inline void dma16(const void *src, void *lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((const GLOBAL void *)src, (LOCAL void *)lds_wave_base, 16,
+                                     0, 0);
+}
+
+/* Reductions over the 16 lanes of a DPP row (one MFMA column group). */
+template <int CTRL> __device__ static inline float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ static inline float row16_max(float v) {
+    v = fmaxf(v, dppf<0xB1>(v));  /* quad_perm [1,0,3,2] */
+    v = fmaxf(v, dppf<0x4E>(v));  /* quad_perm [2,3,0,1] */
+    v = fmaxf(v, dppf<0x141>(v)); /* row_half_mirror */
+    return fmaxf(v, dppf<0x140>(v)); /* row_mirror */
+}
+__device__ static inline float row16_sum(float v) {
+    v += dppf<0xB1>(v);
+    v += dppf<0x4E>(v);
+    v += dppf<0x141>(v);
+    return v + dppf<0x140>(v);
+}
+
+/* Partial row layout: [m, l, 256 columns in MFMA output order]. */
+#define PSTRIDE 258u
+
+/* Head dimension held by output column col (MFMA order) of a wave's tiles:
+ * q8_0 tiles pair even/odd dims of one 32-block (the two bytes a 16-bit LDS
+ * read returns), f16/f32 tiles are 16 consecutive dims. */
+template <int KIND> __device__ static inline uint32_t col_dim(uint32_t col) {
+    if (KIND != Q4KV_Q8) return col;
+    const uint32_t w = col >> 6, t = (col >> 4) & 3u, n = col & 15u;
+    return 32u * (2u * w + (t >> 1)) + 2u * n + (t & 1u);
+}
+
 template <int KIND, int MODE, int HG>
 __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
     constexpr uint32_t CP = KCfg<KIND>::CP;
     constexpr uint32_t RMAX = KCfg<KIND>::RMAX;
-    constexpr uint32_t NH = HG * 8u; /* query-head slots */
+    constexpr uint32_t NH = HG * 8u;     /* query-head slots */
+    constexpr uint32_t NQW = CP / 16u;   /* waves computing scores */
     constexpr uint32_t NLD = (CP * RMAX / 16u + 255u) / 256u;
     __shared__ __attribute__((aligned(16))) uint8_t kraw[CP * RMAX];
     __shared__ __attribute__((aligned(16))) uint8_t vraw[CP * RMAX];
     __shared__ __attribute__((aligned(16))) float sc[NH * CP];
     __shared__ __attribute__((aligned(16))) float vsc[KIND == Q4KV_Q8 ? 8u * CP : 4u];
     __shared__ int32_t s_pos[CP];
-    __shared__ float s_m[NH], s_l[NH], s_al[NH];
+    __shared__ float s_cmax[NQW][NH], s_psum[NQW][NH];
 
+    TRACE(0);
     const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t hd = a.hd, NB = hd / 32u, gqa = a.n_head / a.n_kvh;
@@ -198,141 +297,194 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
     const Item it = resolve_item<MODE>(a, item);
     const uint32_t rowb =
         KIND == Q4KV_Q8 ? NB * 34u : hd * (KIND == Q4KV_F16 ? 2u : 4u);
+    /* LDS row stride: rows packed back to back when 16-byte granular (the
+     * DMA writes contiguous 16-byte chunks), padded otherwise. */
     const uint32_t RS = (rowb + 15u) & ~15u;
     const bool al16 =
         (rowb & 15u) == 0 && ((((uintptr_t)it.kc) | ((uintptr_t)it.vc)) & 15u) == 0;
     const uint32_t n_chunks = (it.n + CP - 1u) / CP;
     const uint32_t c0 = s * a.cps;
     const uint32_t c1 = (s + 1u == a.S) ? n_chunks : min(c0 + a.cps, n_chunks);
+    const uint32_t nch = rowb / 16u, total = CP * nch;
 
     const uint32_t mrow = lane & 15u; /* MFMA A row / B,C column */
-    const uint32_t jg = lane >> 4;    /* MFMA k-group */
+    const uint32_t jg = lane >> 4;    /* MFMA k-group; C rows 4jg..4jg+3 */
     const bool lo_row = mrow >= 8u;
 
-    /* Q operands, hi/lo split across the row halves. */
+    /* ---- positions of the first chunk: all index loads in flight at once ---- */
+    /* pidx[0..NLD) = rows this lane DMAs, pidx[NLD] = s_pos entry tid */
+    int32_t pidx[NLD + 1];
+    uint32_t jrow[NLD + 1];
+#pragma unroll
+    for (uint32_t u = 0; u < NLD; u++) {
+        const uint32_t e = (wave + 4u * u) * 64u + lane;
+        jrow[u] = e < total ? e / nch : 0u;
+    }
+    jrow[NLD] = tid < CP ? tid : 0u;
+    uint32_t jcur[NLD + 1];
+    int32_t raw[NLD + 1];
+#pragma unroll
+    for (uint32_t u = 0; u <= NLD; u++) {
+        jcur[u] = c0 * CP + jrow[u];
+        raw[u] = -1;
+    }
+    if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
+
+    /* ---- Q operands straight from global (8-byte loads), hi/lo split
+     * across the row halves; overlaps the index round trip ---- */
     h8_t qa[HG][8];
+    /* raw fp32 pairs (all loads in flight together), split in the first
+     * chunk once the row DMAs are issued */
+    fv2 qv[HG][8][4];
+    {
+        const float *qh[HG];
 #pragma unroll
-    for (uint32_t hg = 0; hg < HG; hg++) {
-        const uint32_t g = hg * 8u + (mrow & 7u);
+        for (uint32_t hg = 0; hg < HG; hg++) {
+            const uint32_t g = hg * 8u + (mrow & 7u);
+            qh[hg] = it.q + (size_t)(g < gqa ? g : 0u) * hd;
+        }
+        if ((((uintptr_t)it.q) & 7u) == 0) {
 #pragma unroll
-        for (uint32_t b = 0; b < 8u; b++) {
+            for (uint32_t hg = 0; hg < HG; hg++)
 #pragma unroll
-            for (uint32_t i = 0; i < 8u; i++) {
-                float x = 0.f;
-                if (b < NB && g < gqa) {
-                    const uint32_t d = KIND == Q4KV_Q8 ? q8_kdim(b, jg, i) : 8u * jg + i;
-                    x = it.q[(size_t)g * hd + 32u * b + d];
-                }
-                qa[hg][b][i] = split_hl(x, lo_row);
-            }
+                for (uint32_t b = 0; b < 8u; b++)
+#pragma unroll
+                    for (uint32_t k = 0; k < 4u; k++) {
+                        const uint32_t d =
+                            KIND == Q4KV_Q8 ? q8_kdim(b, jg, 2u * k) : 8u * jg + 2u * k;
+                        /* blocks beyond hd re-read block 0 and are zeroed below */
+                        qv[hg][b][k] = ldg((const fv2 *)(qh[hg] + 32u * (b < NB ? b : 0u) + d));
+                    }
+        } else {
+#pragma unroll
+            for (uint32_t hg = 0; hg < HG; hg++)
+#pragma unroll
+                for (uint32_t b = 0; b < 8u; b++)
+#pragma unroll
+                    for (uint32_t k = 0; k < 4u; k++) {
+                        const uint32_t d =
+                            KIND == Q4KV_Q8 ? q8_kdim(b, jg, 2u * k) : 8u * jg + 2u * k;
+                        const float *pq = qh[hg] + 32u * (b < NB ? b : 0u) + d;
+                        qv[hg][b][k][0] = ldg(pq);
+                        qv[hg][b][k][1] = ldg(pq + 1);
+                    }
         }
     }
-    if (tid < NH) {
-        s_m[tid] = -INFINITY;
-        s_l[tid] = 0.f;
-        s_al[tid] = 1.f;
-    }
+
+    /* running max (base 2) and sum of the heads of this lane's C rows */
+    float m_run[HG][4], l_run[HG][4];
     f4_t acc[HG][4];
 #pragma unroll
     for (uint32_t hg = 0; hg < HG; hg++)
 #pragma unroll
-        for (uint32_t t = 0; t < 4u; t++) acc[hg][t] = (f4_t){0.f, 0.f, 0.f, 0.f};
-    __syncthreads();
+        for (uint32_t i = 0; i < 4u; i++) {
+            m_run[hg][i] = -INFINITY;
+            l_run[hg][i] = 0.f;
+            acc[hg][i] = (f4_t){0.f, 0.f, 0.f, 0.f};
+        }
+    TRACE(1);
 
     for (uint32_t c = c0; c < c1; c++) {
         const uint32_t base = c * CP;
-        if (tid < CP) {
-            const uint32_t j = base + tid;
-            int32_t p = -1;
-            if (j < it.n) {
-                p = it.list ? it.list[j] : (int32_t)j;
-                if (p < 0 || (uint32_t)p >= it.max_kv) p = -1;
-            }
-            s_pos[tid] = p;
-        }
-        __syncthreads();
-        /* ---- stage raw K/V rows; invalid positions read row 0 (masked) ---- */
+        pos_finish<NLD + 1, MODE>(it, jcur, raw, pidx);
+        if (tid < CP) s_pos[tid] = pidx[NLD];
+        /* ---- K/V rows of this chunk -> LDS; invalid positions read row 0
+         * (their scores are masked) ---- */
         if (al16) {
-            const uint32_t nch = rowb / 16u, total = CP * nch;
-            uint4 kr[NLD], vr[NLD];
 #pragma unroll
             for (uint32_t u = 0; u < NLD; u++) {
-                const uint32_t e = tid + u * 256u;
+                const uint32_t e0 = (wave + 4u * u) * 64u, e = e0 + lane;
                 if (e < total) {
                     const uint32_t r = e / nch, q = e - r * nch;
-                    int32_t p = s_pos[r];
-                    p = p < 0 ? 0 : p;
+                    const int32_t p = pidx[u] < 0 ? 0 : pidx[u];
                     const size_t off = ((size_t)p * a.n_kvh + kh) * rowb + q * 16u;
-                    kr[u] = *(const uint4 *)(it.kc + off);
-                    vr[u] = *(const uint4 *)(it.vc + off);
-                }
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < NLD; u++) {
-                const uint32_t e = tid + u * 256u;
-                if (e < total) {
-                    const uint32_t r = e / nch, q = e - r * nch;
-                    *(uint4 *)(kraw + r * RS + q * 16u) = kr[u];
-                    *(uint4 *)(vraw + r * RS + q * 16u) = vr[u];
+                    dma16(it.kc + off, kraw + e0 * 16u);
+                    dma16(it.vc + off, vraw + e0 * 16u);
                 }
             }
         } else {
-            const uint32_t nh = rowb / 2u, total = CP * nh;
-            for (uint32_t e = tid; e < total; e += 256u) {
+            const uint32_t nh = rowb / 2u;
+            for (uint32_t e = tid; e < CP * nh; e += 256u) {
                 const uint32_t r = e / nh, q = e - r * nh;
-                int32_t p = s_pos[r];
+                int32_t p = item_pos(it, base + r);
                 p = p < 0 ? 0 : p;
                 const size_t off = ((size_t)p * a.n_kvh + kh) * rowb + q * 2u;
-                *(uint16_t *)(kraw + r * RS + q * 2u) = *(const uint16_t *)(it.kc + off);
-                *(uint16_t *)(vraw + r * RS + q * 2u) = *(const uint16_t *)(it.vc + off);
+                *(uint16_t *)(kraw + r * RS + q * 2u) = ldg((const uint16_t *)(it.kc + off));
+                *(uint16_t *)(vraw + r * RS + q * 2u) = ldg((const uint16_t *)(it.vc + off));
             }
         }
+        if (c == c0) {
+#pragma unroll
+            for (uint32_t hg = 0; hg < HG; hg++) {
+                const uint32_t g = hg * 8u + (mrow & 7u);
+#pragma unroll
+                for (uint32_t b = 0; b < 8u; b++) {
+                    const float qscale = (g < gqa && b < NB) ? 1.f : 0.f;
+#pragma unroll
+                    for (uint32_t k = 0; k < 4u; k++) {
+                        qa[hg][b][2u * k] = split_hl(qv[hg][b][k][0] * qscale, lo_row);
+                        qa[hg][b][2u * k + 1u] = split_hl(qv[hg][b][k][1] * qscale, lo_row);
+                    }
+                }
+            }
+        }
+        TRACE(2);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        TRACE(3);
+        /* ---- prefetch the next chunk's positions (lands during compute) ---- */
+        if (c + 1u < c1) {
+#pragma unroll
+            for (uint32_t u = 0; u <= NLD; u++) jcur[u] = base + CP + jrow[u];
+            pos_issue<NLD + 1, MODE>(it, jcur, raw);
+        }
         if (KIND == Q4KV_Q8) {
             for (uint32_t e = tid; e < NB * CP; e += 256u) {
                 const uint32_t b = e / CP, r = e - b * CP;
                 vsc[b * CP + r] = s_pos[r] < 0 ? 0.f : ld_f16(vraw + r * RS + 34u * b);
             }
         }
-        /* ---- scores: wave w owns positions 16w .. 16w+15 ---- */
-        if (wave * 16u < CP) {
-            const uint32_t r = wave * 16u + mrow;
+        /* ---- scores for positions 16w .. 16w+15, chunk max per head ---- */
+        f4_t T[HG];
+        const uint32_t r = wave * 16u + mrow;
+        if (wave < NQW) {
             const uint8_t *krow = kraw + r * RS;
             f4_t S[HG];
 #pragma unroll
             for (uint32_t hg = 0; hg < HG; hg++) S[hg] = (f4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (uint32_t b = 0; b < 8u; b++) {
-                if (b >= NB) break;
-                if (KIND == Q4KV_Q8) {
-                    const h8_t kb = load_k_q8(krow, b, jg);
-                    const float ks = ld_f16(krow + 34u * b);
+                if (b < NB) {
+                    if (KIND == Q4KV_Q8) {
+                        const h8_t kb = load_k_q8(krow, b, jg);
+                        const float ks = ld_f16(krow + 34u * b);
 #pragma unroll
-                    for (uint32_t hg = 0; hg < HG; hg++) {
-                        f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            qa[hg][b], kb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        S[hg] += ks * C;
-                    }
-                } else if (KIND == Q4KV_F16) {
-                    const h8_t kb = *(const h8_t *)(krow + 64u * b + 16u * jg);
+                        for (uint32_t hg = 0; hg < HG; hg++) {
+                            f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                qa[hg][b], kb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                            S[hg] += ks * C;
+                        }
+                    } else if (KIND == Q4KV_F16) {
+                        const h8_t kb = *(const h8_t *)(krow + 64u * b + 16u * jg);
 #pragma unroll
-                    for (uint32_t hg = 0; hg < HG; hg++)
-                        S[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[hg][b], kb, S[hg],
-                                                                       0, 0, 0);
-                } else {
-                    const float *kf = (const float *)(krow + 128u * b + 32u * jg);
-                    h8_t kh8, kl8;
+                        for (uint32_t hg = 0; hg < HG; hg++)
+                            S[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[hg][b], kb,
+                                                                           S[hg], 0, 0, 0);
+                    } else {
+                        const float *kf = (const float *)(krow + 128u * b + 32u * jg);
+                        h8_t kh8, kl8;
 #pragma unroll
-                    for (uint32_t i = 0; i < 8u; i++) {
-                        kh8[i] = split_hl(kf[i], false);
-                        kl8[i] = split_hl(kf[i], true);
-                    }
+                        for (uint32_t i = 0; i < 8u; i++) {
+                            kh8[i] = split_hl(kf[i], false);
+                            kl8[i] = split_hl(kf[i], true);
+                        }
 #pragma unroll
-                    for (uint32_t hg = 0; hg < HG; hg++) {
-                        S[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[hg][b], kh8, S[hg],
-                                                                       0, 0, 0);
-                        S[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[hg][b], kl8, S[hg],
-                                                                       0, 0, 0);
+                        for (uint32_t hg = 0; hg < HG; hg++) {
+                            S[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[hg][b], kh8,
+                                                                           S[hg], 0, 0, 0);
+                            S[hg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[hg][b], kl8,
+                                                                           S[hg], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -342,38 +494,56 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
 #pragma unroll
                 for (uint32_t i = 0; i < 4u; i++) {
                     const float tot = S[hg][i] + xor32(S[hg][i]);
-                    const uint32_t head = hg * 8u + 4u * jg + i;
-                    if (lane < 32u && head < gqa)
-                        sc[head * CP + r] = valid ? tot * a.scale_log2 : -INFINITY;
+                    T[hg][i] = valid ? tot * a.scale_log2 : -INFINITY;
+                    const float cm = row16_max(T[hg][i]);
+                    if (mrow == 0 && jg < 2u) s_cmax[wave][hg * 8u + 4u * jg + i] = cm;
                 }
             }
         }
+        TRACE(4);
         __syncthreads();
-        /* ---- online softmax statistics, one wave per head ---- */
-        for (uint32_t g = wave; g < gqa; g += 4u) {
-            const float v = lane < CP ? sc[g * CP + lane] : -INFINITY;
-            const float cm = wave_max(v);
-            const float mo = s_m[g];
-            const float mn = fmaxf(mo, cm);
-            const float al = mo == -INFINITY ? 0.f : exp2f(mo - mn);
-            const float w = v == -INFINITY ? 0.f : exp2f(v - mn);
-            if (lane < CP) sc[g * CP + lane] = w;
-            const float ls = wave_sum(w);
-            if (lane == 0) {
-                s_m[g] = mn;
-                s_l[g] = s_l[g] * al + ls;
-                s_al[g] = al;
-            }
-        }
-        __syncthreads();
-        /* ---- P.V: wave w owns head dims 64w .. 64w+63 ---- */
+        TRACE(5);
+        /* ---- new running max for this lane's heads; weights of this chunk ---- */
+        float alpha[HG][4];
 #pragma unroll
         for (uint32_t hg = 0; hg < HG; hg++)
 #pragma unroll
             for (uint32_t i = 0; i < 4u; i++) {
-                const float al = s_al[hg * 8u + ((4u * jg + i) & 7u)];
+                const uint32_t h = hg * 8u + ((4u * jg + i) & 7u);
+                float cm = s_cmax[0][h];
 #pragma unroll
-                for (uint32_t t = 0; t < 4u; t++) acc[hg][t][i] *= al;
+                for (uint32_t w = 1; w < NQW; w++) cm = fmaxf(cm, s_cmax[w][h]);
+                const float mn = fmaxf(m_run[hg][i], cm);
+                alpha[hg][i] = m_run[hg][i] == -INFINITY ? 0.f : exp2f(m_run[hg][i] - mn);
+                m_run[hg][i] = mn;
+            }
+        if (wave < NQW) {
+#pragma unroll
+            for (uint32_t hg = 0; hg < HG; hg++)
+#pragma unroll
+                for (uint32_t i = 0; i < 4u; i++) {
+                    const float w = T[hg][i] == -INFINITY ? 0.f : exp2f(T[hg][i] - m_run[hg][i]);
+                    const uint32_t h = hg * 8u + 4u * jg + i;
+                    if (lane < 32u) sc[h * CP + r] = w;
+                    const float ps = row16_sum(w);
+                    if (mrow == 0 && jg < 2u) s_psum[wave][h] = ps;
+                }
+        }
+        TRACE(6);
+        __syncthreads();
+        TRACE(7);
+        /* ---- running sums; P.V with wave w owning head dims 64w .. 64w+63 ---- */
+#pragma unroll
+        for (uint32_t hg = 0; hg < HG; hg++)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                const uint32_t h = hg * 8u + ((4u * jg + i) & 7u);
+                float ps = 0.f;
+#pragma unroll
+                for (uint32_t w = 0; w < NQW; w++) ps += s_psum[w][h];
+                l_run[hg][i] = l_run[hg][i] * alpha[hg][i] + ps;
+#pragma unroll
+                for (uint32_t t = 0; t < 4u; t++) acc[hg][t][i] *= alpha[hg][i];
             }
 #pragma unroll
         for (uint32_t kc = 0; kc < CP / 32u; kc++) {
@@ -382,33 +552,34 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
 #pragma unroll
                 for (uint32_t u = 0; u < 2u; u++) {
                     const uint32_t bb = 2u * wave + u;
-                    if (bb >= NB) break;
-                    /* B: dims 32bb + 2n (tile 0) and 32bb + 2n + 1 (tile 1). */
-                    const uint8_t *vb = vraw + p0 * RS + 34u * bb + 2u + 2u * mrow;
-                    u4_t r0, r1;
+                    if (bb < NB) {
+                        /* B: dims 32bb + 2n (tile 0) and 32bb + 2n + 1 (tile 1). */
+                        const uint8_t *vb = vraw + p0 * RS + 34u * bb + 2u + 2u * mrow;
+                        u4_t r0, r1;
 #pragma unroll
-                    for (uint32_t k = 0; k < 4u; k++) {
-                        uint32_t x = (uint32_t)*(const uint16_t *)(vb + (2u * k) * RS) |
-                                     ((uint32_t)*(const uint16_t *)(vb + (2u * k + 1u) * RS)
-                                      << 16);
-                        x ^= 0x80808080u;
-                        r0[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04020400u);
-                        r1[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04030401u);
-                    }
-                    const h8_t B0 = h8_minus_1152(r0), B1 = h8_minus_1152(r1);
-                    const float *sp = vsc + bb * CP + p0;
+                        for (uint32_t k = 0; k < 4u; k++) {
+                            uint32_t x =
+                                (uint32_t)*(const uint16_t *)(vb + (2u * k) * RS) |
+                                ((uint32_t)*(const uint16_t *)(vb + (2u * k + 1u) * RS) << 16);
+                            x ^= 0x80808080u;
+                            r0[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04020400u);
+                            r1[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04030401u);
+                        }
+                        const h8_t B0 = h8_minus_1152(r0), B1 = h8_minus_1152(r1);
+                        const float *sp = vsc + bb * CP + p0;
 #pragma unroll
-                    for (uint32_t hg = 0; hg < HG; hg++) {
-                        const uint32_t head = hg * 8u + (mrow & 7u);
-                        const float *wp = sc + head * CP + p0;
-                        h8_t A;
+                        for (uint32_t hg = 0; hg < HG; hg++) {
+                            const uint32_t head = hg * 8u + (mrow & 7u);
+                            const float *wp = sc + head * CP + p0;
+                            h8_t A;
 #pragma unroll
-                        for (uint32_t i = 0; i < 8u; i++)
-                            A[i] = split_hl(head < gqa ? wp[i] * sp[i] : 0.f, lo_row);
-                        acc[hg][2u * u] =
-                            __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B0, acc[hg][2u * u], 0, 0, 0);
-                        acc[hg][2u * u + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            A, B1, acc[hg][2u * u + 1u], 0, 0, 0);
+                            for (uint32_t i = 0; i < 8u; i++)
+                                A[i] = split_hl(head < gqa ? wp[i] * sp[i] : 0.f, lo_row);
+                            acc[hg][2u * u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                A, B0, acc[hg][2u * u], 0, 0, 0);
+                            acc[hg][2u * u + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                A, B1, acc[hg][2u * u + 1u], 0, 0, 0);
+                        }
                     }
                 }
             } else {
@@ -424,115 +595,433 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
 #pragma unroll
                 for (uint32_t t = 0; t < 4u; t++) {
                     const uint32_t dim = 64u * wave + 16u * t + mrow;
-                    if (64u * wave + 16u * t >= hd) break;
-                    if (KIND == Q4KV_F16) {
-                        const uint8_t *vb = vraw + p0 * RS + 2u * dim;
-                        u4_t r;
+                    if (64u * wave + 16u * t < hd) {
+                        if (KIND == Q4KV_F16) {
+                            const uint8_t *vb = vraw + p0 * RS + 2u * dim;
+                            u4_t rr;
 #pragma unroll
-                        for (uint32_t k = 0; k < 4u; k++)
-                            r[k] = (uint32_t)*(const uint16_t *)(vb + (2u * k) * RS) |
-                                   ((uint32_t)*(const uint16_t *)(vb + (2u * k + 1u) * RS) << 16);
-                        const h8_t B = __builtin_bit_cast(h8_t, r);
+                            for (uint32_t k = 0; k < 4u; k++)
+                                rr[k] = (uint32_t)*(const uint16_t *)(vb + (2u * k) * RS) |
+                                        ((uint32_t)*(const uint16_t *)(vb + (2u * k + 1u) * RS)
+                                         << 16);
+                            const h8_t B = __builtin_bit_cast(h8_t, rr);
 #pragma unroll
-                        for (uint32_t hg = 0; hg < HG; hg++)
-                            acc[hg][t] =
-                                __builtin_amdgcn_mfma_f32_16x16x32_f16(A[hg], B, acc[hg][t], 0, 0, 0);
-                    } else {
-                        const uint8_t *vb = vraw + p0 * RS + 4u * dim;
-                        h8_t Bh, Bl;
+                            for (uint32_t hg = 0; hg < HG; hg++)
+                                acc[hg][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    A[hg], B, acc[hg][t], 0, 0, 0);
+                        } else {
+                            const uint8_t *vb = vraw + p0 * RS + 4u * dim;
+                            h8_t Bh, Bl;
 #pragma unroll
-                        for (uint32_t i = 0; i < 8u; i++) {
-                            const float x = *(const float *)(vb + i * RS);
-                            Bh[i] = split_hl(x, false);
-                            Bl[i] = split_hl(x, true);
-                        }
+                            for (uint32_t i = 0; i < 8u; i++) {
+                                const float x = *(const float *)(vb + i * RS);
+                                Bh[i] = split_hl(x, false);
+                                Bl[i] = split_hl(x, true);
+                            }
 #pragma unroll
-                        for (uint32_t hg = 0; hg < HG; hg++) {
-                            acc[hg][t] =
-                                __builtin_amdgcn_mfma_f32_16x16x32_f16(A[hg], Bh, acc[hg][t], 0, 0, 0);
-                            acc[hg][t] =
-                                __builtin_amdgcn_mfma_f32_16x16x32_f16(A[hg], Bl, acc[hg][t], 0, 0, 0);
+                            for (uint32_t hg = 0; hg < HG; hg++) {
+                                acc[hg][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    A[hg], Bh, acc[hg][t], 0, 0, 0);
+                                acc[hg][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    A[hg], Bl, acc[hg][t], 0, 0, 0);
+                            }
                         }
                     }
                 }
             }
         }
+        TRACE(8);
         __syncthreads();
+        TRACE(9);
     }
 
     /* ---- epilogue: fold lo rows into hi rows, then finalise or spill ---- */
     const bool fin = a.S == 1u;
-    const size_t pstride = (size_t)hd + 2u;
-    float *pbase = fin ? nullptr : a.part + ((size_t)item * a.S + s) * gqa * pstride;
+    float *pbase = fin ? nullptr : a.part + ((size_t)item * a.S + s) * gqa * PSTRIDE;
 #pragma unroll
     for (uint32_t hg = 0; hg < HG; hg++) {
 #pragma unroll
         for (uint32_t t = 0; t < 4u; t++) {
-            uint32_t dim;
-            bool dvalid;
-            if (KIND == Q4KV_Q8) {
-                const uint32_t bb = 2u * wave + (t >> 1);
-                dim = 32u * bb + 2u * mrow + (t & 1u);
-                dvalid = bb < NB;
-            } else {
-                dim = 64u * wave + 16u * t + mrow;
-                dvalid = 64u * wave + 16u * t < hd;
-            }
+            const uint32_t col = (wave * 4u + t) * 16u + mrow;
+            const uint32_t dim = col_dim<KIND>(col);
+            const bool dvalid = dim < hd;
 #pragma unroll
             for (uint32_t i = 0; i < 4u; i++) {
                 const float tot = acc[hg][t][i] + xor32(acc[hg][t][i]);
                 const uint32_t head = hg * 8u + 4u * jg + i;
                 if (lane < 32u && dvalid && head < gqa) {
                     if (fin) {
-                        const float l = s_l[head];
-                        float r = l > 0.f ? tot / l : 0.f;
-                        if (it.gate) r *= 1.f / (1.f + expf(-it.gate[(size_t)head * hd + dim]));
-                        it.out[(size_t)head * hd + dim] = r;
+                        const float l = l_run[hg][i];
+                        float rv = l > 0.f ? tot / l : 0.f;
+                        if (it.gate)
+                            rv *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)head * hd + dim)));
+                        stg(it.out + (size_t)head * hd + dim, rv);
                     } else {
-                        pbase[head * pstride + 2u + dim] = tot;
+                        stg(pbase + head * PSTRIDE + 2u + col, tot);
                     }
                 }
             }
         }
+        if (!fin && wave == 0 && mrow == 0 && jg < 2u) {
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                const uint32_t head = hg * 8u + 4u * jg + i;
+                if (head < gqa) {
+                    stg(pbase + head * PSTRIDE, m_run[hg][i]);
+                    stg(pbase + head * PSTRIDE + 1u, l_run[hg][i]);
+                }
+            }
+        }
     }
-    if (!fin && tid < gqa) {
-        pbase[tid * pstride] = s_m[tid];
-        pbase[tid * pstride + 1u] = s_l[tid];
+    TRACE(10);
+}
+
+/* Fast path for the production shape: q8_0 cache, head_dim 256 (272-byte
+ * rows, 17 x 16 B), at most 8 query heads per KV head. Same algorithm as
+ * qsa_attn_k with every shape constant compile-time, the weight hi/lo split
+ * done with mixed-precision FMAs, and the partial / output rows staged
+ * through LDS for 16-byte stores. */
+template <int MODE>
+__global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
+    constexpr uint32_t CP = 64, ROWB = 272, NCH = 17, NLD = 5;
+    __shared__ __attribute__((aligned(16))) uint8_t kraw[CP * ROWB];
+    __shared__ __attribute__((aligned(16))) uint8_t vraw[CP * ROWB];
+    __shared__ __attribute__((aligned(16))) float sw[8 * CP];  /* weights [head][pos] */
+    __shared__ __attribute__((aligned(16))) float vsc[8 * CP]; /* V scales [block][pos] */
+    __shared__ int32_t s_pos[CP];
+    __shared__ float s_cmax[4][8], s_psum[4][8], s_ml[2][8];
+
+    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t gqa = a.n_head / a.n_kvh;
+    const uint32_t kh = item % a.n_kvh;
+    const Item it = resolve_item<MODE>(a, item);
+    const bool al16 = ((((uintptr_t)it.kc) | ((uintptr_t)it.vc)) & 15u) == 0;
+    const uint32_t n_chunks = (it.n + CP - 1u) / CP;
+    const uint32_t c0 = s * a.cps;
+    const uint32_t c1 = (s + 1u == a.S) ? n_chunks : min(c0 + a.cps, n_chunks);
+    const uint32_t mrow = lane & 15u, jg = lane >> 4;
+    const bool lo_row = mrow >= 8u;
+    const size_t rstride = (size_t)a.n_kvh * ROWB; /* bytes per token */
+    const uint8_t *kbase = it.kc + (size_t)kh * ROWB, *vbase = it.vc + (size_t)kh * ROWB;
+
+    /* rows this lane DMAs (u < 4 always valid, u = 4 only in wave 0) and the
+     * s_pos entry of thread tid */
+    uint32_t jcur[NLD + 1];
+    int32_t raw[NLD + 1], pidx[NLD + 1];
+#pragma unroll
+    for (uint32_t u = 0; u < NLD; u++) jcur[u] = c0 * CP + ((wave + 4u * u) * 64u + lane) / NCH;
+    jcur[NLD] = c0 * CP + (tid & (CP - 1u));
+#pragma unroll
+    for (uint32_t u = 0; u <= NLD; u++) raw[u] = -1;
+    if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
+
+    /* Q: 32 eight-byte loads per lane in flight; split after the DMA issue */
+    const uint32_t g = mrow & 7u;
+    const float *qh = it.q + (size_t)(g < gqa ? g : 0u) * 256u;
+    h8_t qa[8];
+    {
+        fv2 qv[8][4];
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++)
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; k++)
+                qv[b][k] = ldg((const fv2 *)(qh + 32u * b + q8_kdim(b, jg, 2u * k)));
+        const float qs = g < gqa ? 1.f : 0.f;
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++)
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; k++) {
+                qa[b][2u * k] = split_hl(qv[b][k][0] * qs, lo_row);
+                qa[b][2u * k + 1u] = split_hl(qv[b][k][1] * qs, lo_row);
+            }
+    }
+
+    float m_run[4], l_run[4];
+    f4_t acc[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; i++) {
+        m_run[i] = -INFINITY;
+        l_run[i] = 0.f;
+        acc[i] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (uint32_t c = c0; c < c1; c++) {
+        pos_finish<NLD + 1, MODE>(it, jcur, raw, pidx);
+        if (tid < CP) s_pos[tid] = pidx[NLD];
+        if (al16) {
+#pragma unroll
+            for (uint32_t u = 0; u < NLD; u++) {
+                const uint32_t e0 = (wave + 4u * u) * 64u, e = e0 + lane;
+                if (u < 4u || wave == 0) {
+                    const uint32_t r = e / NCH, q = e - r * NCH;
+                    const size_t off = (size_t)(pidx[u] < 0 ? 0 : pidx[u]) * rstride + q * 16u;
+                    (void)r;
+                    dma16(kbase + off, kraw + e0 * 16u);
+                    dma16(vbase + off, vraw + e0 * 16u);
+                }
+            }
+        } else {
+            for (uint32_t e = tid; e < CP * (ROWB / 2u); e += 256u) {
+                const uint32_t r = e / (ROWB / 2u), q = e - r * (ROWB / 2u);
+                const int32_t p = item_pos(it, c * CP + r);
+                const size_t off = (size_t)(p < 0 ? 0 : p) * rstride + q * 2u;
+                *(uint16_t *)(kraw + r * ROWB + q * 2u) = ldg((const uint16_t *)(kbase + off));
+                *(uint16_t *)(vraw + r * ROWB + q * 2u) = ldg((const uint16_t *)(vbase + off));
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (c + 1u < c1) {
+#pragma unroll
+            for (uint32_t u = 0; u <= NLD; u++) jcur[u] += CP;
+            pos_issue<NLD + 1, MODE>(it, jcur, raw);
+        }
+        /* V block scales, 0 for masked positions */
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; k++) {
+            const uint32_t e = tid + 256u * k, b = e >> 6, r = e & 63u;
+            vsc[e] = s_pos[r] < 0 ? 0.f : ld_f16(vraw + r * ROWB + 34u * b);
+        }
+        /* ---- scores: wave w, positions 16w .. 16w+15 ---- */
+        const uint32_t r = wave * 16u + mrow;
+        const uint8_t *krow = kraw + r * ROWB;
+        f4_t S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++) {
+            const h8_t kb = load_k_q8(krow, b, jg);
+            const float ks = ld_f16(krow + 34u * b);
+            const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                qa[b], kb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            S += ks * C;
+        }
+        const bool valid = s_pos[r] >= 0;
+        float T[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            T[i] = valid ? (S[i] + xor32(S[i])) * a.scale_log2 : -INFINITY;
+            const float cm = row16_max(T[i]);
+            if (mrow == 0 && jg < 2u) s_cmax[wave][4u * jg + i] = cm;
+        }
+        __syncthreads();
+        float alpha[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            const uint32_t h = (4u * jg + i) & 7u;
+            const float cm = fmaxf(fmaxf(s_cmax[0][h], s_cmax[1][h]),
+                                   fmaxf(s_cmax[2][h], s_cmax[3][h]));
+            const float mn = fmaxf(m_run[i], cm);
+            alpha[i] = m_run[i] == -INFINITY ? 0.f : exp2f(m_run[i] - mn);
+            m_run[i] = mn;
+            const float w = T[i] == -INFINITY ? 0.f : exp2f(T[i] - mn);
+            if (lane < 32u) sw[(4u * jg + i) * CP + r] = w;
+            const float ps = row16_sum(w);
+            if (mrow == 0 && jg < 2u) s_psum[wave][4u * jg + i] = ps;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            const uint32_t h = (4u * jg + i) & 7u;
+            l_run[i] = l_run[i] * alpha[i] + (s_psum[0][h] + s_psum[1][h]) +
+                       (s_psum[2][h] + s_psum[3][h]);
+#pragma unroll
+            for (uint32_t t = 0; t < 4u; t++) acc[t][i] *= alpha[i];
+        }
+        /* ---- P.V: wave w, dims 64w .. 64w+63 (blocks 2w, 2w+1) ---- */
+#pragma unroll
+        for (uint32_t kc = 0; kc < 2u; kc++) {
+            const uint32_t p0 = 32u * kc + 8u * jg;
+            const float *wp = sw + g * CP + p0;
+#pragma unroll
+            for (uint32_t u = 0; u < 2u; u++) {
+                const uint32_t bb = 2u * wave + u;
+                const uint8_t *vb = vraw + p0 * ROWB + 34u * bb + 2u + 2u * mrow;
+                u4_t r0, r1;
+#pragma unroll
+                for (uint32_t k = 0; k < 4u; k++) {
+                    uint32_t x = (uint32_t)*(const uint16_t *)(vb + (2u * k) * ROWB) |
+                                 ((uint32_t)*(const uint16_t *)(vb + (2u * k + 1u) * ROWB) << 16);
+                    x ^= 0x80808080u;
+                    r0[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04020400u);
+                    r1[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04030401u);
+                }
+                const float *sp = vsc + bb * CP + p0;
+                h8_t A;
+#pragma unroll
+                for (uint32_t i = 0; i < 8u; i++) {
+                    const float x = wp[i] * sp[i];
+                    const _Float16 hi = (_Float16)x;
+                    A[i] = lo_row ? (_Float16)__builtin_fmaf(wp[i], sp[i], -(float)hi) : hi;
+                }
+                acc[2u * u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, h8_minus_1152(r0),
+                                                                    acc[2u * u], 0, 0, 0);
+                acc[2u * u + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    A, h8_minus_1152(r1), acc[2u * u + 1u], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    /* ---- epilogue: hi+lo rows -> LDS [head][col], then 16-byte stores ---- */
+    float *so = (float *)kraw; /* 8 x 256 floats, free after the last chunk */
+    if (c0 >= c1) __syncthreads();
+#pragma unroll
+    for (uint32_t t = 0; t < 4u; t++)
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            const float tot = acc[t][i] + xor32(acc[t][i]);
+            if (lane < 32u) so[(4u * jg + i) * 256u + (wave * 4u + t) * 16u + mrow] = tot;
+        }
+    if (wave == 0 && mrow == 0 && jg < 2u) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            s_ml[0][4u * jg + i] = m_run[i];
+            s_ml[1][4u * jg + i] = l_run[i];
+        }
+    }
+    __syncthreads();
+    if (a.S == 1u) {
+        /* thread -> (head, 8 consecutive dims) */
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; k++) {
+            const uint32_t e = tid + 256u * k, h = e >> 6, d0 = (e & 63u) * 4u;
+            if (h < gqa) {
+                const float l = s_ml[1][h];
+                const float inv = l > 0.f ? 1.f / l : 0.f;
+                f4_t o;
+#pragma unroll
+                for (uint32_t j = 0; j < 4u; j++) {
+                    const uint32_t d = d0 + j, bb = d >> 5, w = bb >> 1;
+                    const uint32_t t = 2u * (bb & 1u) + (d & 1u), n = (d & 31u) >> 1;
+                    float rv = so[h * 256u + (w * 4u + t) * 16u + n] * inv;
+                    if (it.gate) rv *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)h * 256u + d)));
+                    o[j] = rv;
+                }
+                stg((f4_t *)(it.out + (size_t)h * 256u + d0), o);
+            }
+        }
+    } else {
+        float *pbase = a.part + ((size_t)item * a.S + s) * gqa * PSTRIDE;
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; k++) {
+            const uint32_t e = tid + 256u * k, h = e >> 6, c4 = (e & 63u) * 4u;
+            if (h < gqa) {
+                const float *src = so + h * 256u + c4;
+                float *dst = pbase + h * PSTRIDE + 2u + c4;
+                /* PSTRIDE rows start 8-byte aligned: two 8-byte stores */
+                stg((fv2 *)dst, (fv2){src[0], src[1]});
+                stg((fv2 *)(dst + 2), (fv2){src[2], src[3]});
+            }
+        }
+        if (tid < gqa) {
+            stg((fv2 *)(pbase + tid * PSTRIDE), (fv2){s_ml[0][tid], s_ml[1][tid]});
+        }
     }
 }
 
 /* Merge the S split partials of one (item, head): weights 2^(m_s - M) over
- * splits with l_s > 0, then the sigmoid gate (src/q4_rocm.cu:6968-7013). */
-template <int MODE>
+ * splits with l_s > 0, then the sigmoid gate (src/q4_rocm.cu:6968-7013).
+ * Thread c owns output column c; for S <= 64 every partial load is issued
+ * up front, so the merge costs one memory round trip. */
+#define COMB_MAXS 1024u
+#define COMB_REG 64u
+template <int KIND, int MODE>
 __global__ __launch_bounds__(256) void qsa_comb_k(AttnArgs a) {
-    const uint32_t g = blockIdx.x, item = a.item0 + blockIdx.y, d = threadIdx.x;
-    const uint32_t gqa = a.n_head / a.n_kvh, hd = a.hd;
+    __shared__ float wsh[COMB_MAXS];
+    __shared__ float red[2][4];
+    const uint32_t g = blockIdx.x, item = a.item0 + blockIdx.y, tid = threadIdx.x;
+    const uint32_t gqa = a.n_head / a.n_kvh, hd = a.hd, S = a.S;
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
     const Item it = resolve_item<MODE>(a, item);
-    const size_t pstride = (size_t)hd + 2u;
-    const float *pb = a.part + ((size_t)item * a.S * gqa + g) * pstride;
-    const size_t sstride = (size_t)gqa * pstride;
+    const float *pb = a.part + ((size_t)item * S * gqa + g) * PSTRIDE;
+    const size_t sst = (size_t)gqa * PSTRIDE;
+    const uint32_t dim = col_dim<KIND>(tid);
+    const bool dvalid = dim < hd;
+    float gate = 1.f;
+    if (it.gate && dvalid) gate = 1.f / (1.f + expf(-ldg(it.gate + (size_t)g * hd + dim)));
+    float v[COMB_REG];
+    if (S <= COMB_REG) {
+#pragma unroll
+        for (uint32_t k = 0; k < COMB_REG; k++)
+            v[k] = (k < S && dvalid) ? ldg(pb + k * sst + 2u + tid) : 0.f;
+    }
+    float mloc[COMB_MAXS / 256u], lloc[COMB_MAXS / 256u];
     float M = -INFINITY;
-    for (uint32_t s = 0; s < a.S; s++) {
-        const float m = pb[s * sstride], l = pb[s * sstride + 1u];
-        if (l > 0.f) M = fmaxf(M, m);
+#pragma unroll
+    for (uint32_t k = 0; k < COMB_MAXS / 256u; k++) {
+        const uint32_t sp = tid + 256u * k;
+        mloc[k] = sp < S ? ldg(pb + sp * sst) : -INFINITY;
+        lloc[k] = sp < S ? ldg(pb + sp * sst + 1u) : 0.f;
     }
-    float L = 0.f, acc = 0.f;
-    for (uint32_t s = 0; s < a.S; s++) {
-        const float l = pb[s * sstride + 1u];
-        if (l > 0.f) {
-            const float w = exp2f(pb[s * sstride] - M);
-            L += w * l;
-            if (d < hd) acc += w * pb[s * sstride + 2u + d];
-        }
+#pragma unroll
+    for (uint32_t k = 0; k < COMB_MAXS / 256u; k++)
+        if (lloc[k] > 0.f) M = fmaxf(M, mloc[k]);
+    M = wave_max(M);
+    if (lane == 0) red[0][wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float L = 0.f;
+#pragma unroll
+    for (uint32_t k = 0; k < COMB_MAXS / 256u; k++) {
+        const uint32_t sp = tid + 256u * k;
+        const float w = lloc[k] > 0.f ? exp2f(mloc[k] - M) : 0.f;
+        if (sp < S) wsh[sp] = w;
+        L += w * lloc[k];
     }
-    if (d < hd) {
-        float r = L > 0.f ? acc / L : 0.f;
-        if (it.gate) r *= 1.f / (1.f + expf(-it.gate[(size_t)g * hd + d]));
-        it.out[(size_t)g * hd + d] = r;
+    L = wave_sum(L);
+    if (lane == 0) red[1][wave] = L;
+    __syncthreads();
+    L = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    if (!dvalid) return;
+    float acc = 0.f;
+    if (S <= COMB_REG) {
+#pragma unroll
+        for (uint32_t k = 0; k < COMB_REG; k++)
+            if (k < S) acc += wsh[k] * v[k];
+    } else {
+        for (uint32_t sp = 0; sp < S; sp++) acc += wsh[sp] * ldg(pb + sp * sst + 2u + tid);
     }
+    const float r = L > 0.f ? acc / L * gate : 0.f;
+    stg(it.out + (size_t)g * hd + dim, r);
 }
 
 /* ------------------------------------------------------------------------ */
+
+/* Live timing of the split-KV kernel: HIP events recorded on the library
+ * stream around each launch while armed (never inside a capture). */
+#define Q4KV_PROF_MAX 4096
+static hipEvent_t g_pev[2 * Q4KV_PROF_MAX];
+static int g_pev_made = 0, g_prof_on = 0, g_prof_n = 0, g_prof_max = 0;
+
+extern "C" bool q4kv_prof_begin(int max_launches) {
+    if (!q4kv_ok || q4kv_capturing || max_launches <= 0 || max_launches > Q4KV_PROF_MAX)
+        return false;
+    for (; g_pev_made < 2 * max_launches; g_pev_made++)
+        if (hipEventCreate(&g_pev[g_pev_made]) != hipSuccess) return false;
+    g_prof_on = 1;
+    g_prof_n = 0;
+    g_prof_max = max_launches;
+    return true;
+}
+
+extern "C" int q4kv_prof_end(double *total_ms) {
+    g_prof_on = 0;
+    if (total_ms) *total_ms = 0.0;
+    if (!g_prof_n) return 0;
+    if (hipEventSynchronize(g_pev[2 * g_prof_n - 1]) != hipSuccess) return -1;
+    double t = 0.0;
+    for (int i = 0; i < g_prof_n; i++) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, g_pev[2 * i], g_pev[2 * i + 1]) != hipSuccess) return -1;
+        t += ms;
+    }
+    if (total_ms) *total_ms = t;
+    return g_prof_n;
+}
+
+static inline bool prof_armed(void) {
+    return g_prof_on && !q4kv_capturing && g_prof_n < g_prof_max;
+}
 
 #define Q4KV_TARGET_WG 2048u /* aim for >= 8 workgroups per CU */
 #define Q4KV_MAX_GRID_Y 65535u
@@ -544,7 +1033,8 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
     uint32_t S = (Q4KV_TARGET_WG + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
-    const size_t per = (size_t)gqa * (a.hd + 2u);
+    if (S > COMB_MAXS) S = COMB_MAXS;
+    const size_t per = (size_t)gqa * PSTRIDE;
     while (S > 1u && (size_t)n_items * S * per > q4kv_part_cap) S--;
     if (!q4kv_part) S = 1u;
     const uint32_t cps = n_chunks ? (n_chunks + S - 1u) / S : 1u;
@@ -557,11 +1047,16 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         const uint32_t ni = n_items - i0 < Q4KV_MAX_GRID_Y ? n_items - i0 : Q4KV_MAX_GRID_Y;
         a.item0 = i0;
         dim3 grid(S, ni);
-        if (gqa <= 8u)
+        const bool prof = prof_armed();
+        if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
+        if (KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u)
+            qsa_q8d256_k<MODE><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (gqa <= 8u)
             qsa_attn_k<KIND, MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
         else
             qsa_attn_k<KIND, MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
-        if (S > 1u) qsa_comb_k<MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
+        if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n++ + 1], q4kv_stream);
+        if (S > 1u) qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
     }
     return q4kv_launch_ok("qsa attention");
 }
@@ -667,5 +1162,13 @@ extern "C" bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n
     a.seqs = d_descs;
     return launch_attn<MODE_BATCH>(kv_f16, a, n_seq * n_kvh, max_n);
 }
+
+#ifdef Q4KV_TRACE
+extern "C" int q4kv_trace_read(uint64_t *host, size_t n) {
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(q4kv_trace_buf), n * sizeof(uint64_t), 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
 
 extern "C" bool q4_hip_qsa_topk_alloc(void) { return q4kv_ok && q4kv_part != nullptr; }

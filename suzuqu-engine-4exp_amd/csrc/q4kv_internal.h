@@ -20,6 +20,14 @@ extern int32_t *q4kv_pos_d;
 extern float *q4kv_part;
 extern size_t q4kv_part_cap;
 
+#define GLOBAL __attribute__((address_space(1)))
+#define LOCAL __attribute__((address_space(3)))
+/* Loads/stores through the global address space: pointers taken from
+ * argument structs and descriptors would otherwise compile to flat
+ * accesses, whose waits also cover LDS traffic. */
+template <class T> __device__ static inline T ldg(const T *p) { return *(const GLOBAL T *)p; }
+template <class T> __device__ static inline void stg(T *p, T v) { *(GLOBAL T *)p = v; }
+
 #define Q4KV_ERR(...)                                                          \
     do {                                                                       \
         fprintf(stderr, "q4 hip: " __VA_ARGS__);                               \

@@ -22,6 +22,9 @@ extern "C" {
 #include "q4kv.h"
 }
 
+typedef float fv4 __attribute__((ext_vector_type(4)));
+typedef uint32_t uv4 __attribute__((ext_vector_type(4)));
+
 #define QBLK_PER_WG 32u /* 256 threads / 8 lanes per block */
 
 /* Quantise blocks [blk0, blk0+32) of src into dst (block-indexed). */
@@ -36,10 +39,10 @@ __device__ static void q8_quant_wg(const float *__restrict__ src, uint8_t *__res
     if (live) {
         const float *p = src + b * 32u + part * 4u;
         if (src_al16) {
-            float4 v = *(const float4 *)p;
-            x0 = v.x; x1 = v.y; x2 = v.z; x3 = v.w;
+            const fv4 v = ldg((const fv4 *)p);
+            x0 = v[0]; x1 = v[1]; x2 = v[2]; x3 = v[3];
         } else {
-            x0 = p[0]; x1 = p[1]; x2 = p[2]; x3 = p[3];
+            x0 = ldg(p); x1 = ldg(p + 1); x2 = ldg(p + 2); x3 = ldg(p + 3);
         }
     }
     float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
@@ -66,9 +69,9 @@ __device__ static void q8_quant_wg(const float *__restrict__ src, uint8_t *__res
     const uint64_t nb = nblocks - blk0 < QBLK_PER_WG ? nblocks - blk0 : QBLK_PER_WG;
     uint8_t *out = dst + blk0 * 34u;
     if (dst_al16 && nb == QBLK_PER_WG) {
-        if (t < QBLK_PER_WG * 34u / 16u) ((uint4 *)out)[t] = ((const uint4 *)ob)[t];
+        if (t < QBLK_PER_WG * 34u / 16u) stg((uv4 *)out + t, ((const uv4 *)ob)[t]);
     } else {
-        for (uint32_t i = t; i < nb * 34u; i += blockDim.x) out[i] = ob[i];
+        for (uint32_t i = t; i < nb * 34u; i += blockDim.x) stg(out + i, ob[i]);
     }
 }
 
@@ -124,6 +127,42 @@ __global__ __launch_bounds__(256) static void kv_append_k(const float *__restric
                 ((float *)dst)[i] = src[i];
         }
     }
+}
+
+/* One launch appending a token's rows into several caches (layers or
+ * sequences): grid.z selects the descriptor. Each descriptor carries its own
+ * caches, fp32 rows and token position, so no device position is needed. */
+__global__ __launch_bounds__(256) static void kv_append_batch_k(const q4kv_append_desc *__restrict__ ds,
+                                                                uint32_t n, uint32_t bpt, int kind) {
+    const q4kv_append_desc *d = ds + blockIdx.z;
+    const size_t off = (size_t)ldg(&d->pos) * bpt;
+    const float *src = blockIdx.y ? ldg(&d->v) : ldg(&d->k);
+    uint8_t *dst = (uint8_t *)(blockIdx.y ? ldg(&d->vcache) : ldg(&d->kcache)) + off;
+    if (kind == Q4KV_Q8) {
+        const bool s_al = ((uintptr_t)src & 15u) == 0;
+        const bool d_al = ((uintptr_t)dst & 15u) == 0;
+        q8_quant_wg(src, dst, n / 32u, (uint64_t)blockIdx.x * QBLK_PER_WG, s_al, d_al);
+    } else {
+        for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n;
+             i += gridDim.x * blockDim.x) {
+            if (kind == Q4KV_F16)
+                stg((uint16_t *)dst + i, __half_as_ushort(__float2half_rn(ldg(src + i))));
+            else
+                stg((float *)dst + i, ldg(src + i));
+        }
+    }
+}
+
+extern "C" bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc,
+                                       uint32_t n, uint32_t bpt, int kind) {
+    if (!q4kv_ok || !d_descs || !n_desc || !n || !bpt || n_desc > 65535u) return false;
+    if (kind < Q4KV_F32 || kind > Q4KV_Q8) return false;
+    if (kind == Q4KV_Q8 && (n % 32u)) return false;
+    (void)hipGetLastError();
+    const uint32_t gx = kind == Q4KV_Q8 ? (n / 32u + QBLK_PER_WG - 1) / QBLK_PER_WG
+                                        : (n + 255u) / 256u;
+    kv_append_batch_k<<<dim3(gx, 2, n_desc), 256, 0, q4kv_stream>>>(d_descs, n, bpt, kind);
+    return q4kv_launch_ok("kv_append_batch");
 }
 
 extern "C" bool q4_hip_f32_to_q8(void *dst_q8, const float *src, uint64_t n) {

@@ -36,6 +36,13 @@ class SeqDesc(C.Structure):
 assert C.sizeof(SeqDesc) == 64
 
 
+class AppendDesc(C.Structure):
+    """q4kv_append_desc of include/q4kv.h (40 bytes)."""
+
+    _fields_ = [("kcache", _vp), ("vcache", _vp), ("k", _vp), ("v", _vp), ("pos", _u32),
+                ("reserved", _u32)]
+
+
 class KvCache(C.Structure):
     """q4kv_cache of include/q4kv_host.h."""
 
@@ -88,6 +95,9 @@ SIGNATURES = {
     "q4kv_timer_end_ms": (C.c_double, [C.c_int]),
     "q4kv_device_info": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_int),
                                    C.POINTER(C.c_int)]),
+    "q4kv_prof_begin": (_b, [C.c_int]),
+    "q4kv_prof_end": (C.c_int, [C.POINTER(C.c_double)]),
+    "q4_hip_kv_append_batch": (_b, [_vp, _u32, _u32, _u32, C.c_int]),
     # host layer (include/q4kv_host.h)
     "q4kv_kind_of": (C.c_int, [C.c_char_p]),
     "q4kv_token_bytes": (_u32, [C.c_int, _u32, _u32]),
