@@ -682,15 +682,18 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
  * done with mixed-precision FMAs, and the partial / output rows staged
  * through LDS for 16-byte stores. */
 template <int MODE>
-__global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
+__global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
     constexpr uint32_t CP = 64, ROWB = 272, NCH = 17, NLD = 5;
     __shared__ __attribute__((aligned(16))) uint8_t kraw[CP * ROWB];
     __shared__ __attribute__((aligned(16))) uint8_t vraw[CP * ROWB];
     __shared__ __attribute__((aligned(16))) float sw[8 * CP];  /* weights [head][pos] */
     __shared__ __attribute__((aligned(16))) float vsc[8 * CP]; /* V scales [block][pos] */
+    /* raw fp32 Q rows, 1040-byte stride (4 pad floats) against bank conflicts */
+    __shared__ __attribute__((aligned(16))) float qraw[8 * 260];
     __shared__ int32_t s_pos[CP];
     __shared__ float s_cmax[4][8], s_psum[4][8], s_ml[2][8];
 
+    TRACE(0);
     const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t gqa = a.n_head / a.n_kvh;
@@ -716,27 +719,18 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
     for (uint32_t u = 0; u <= NLD; u++) raw[u] = -1;
     if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
 
-    /* Q: 32 eight-byte loads per lane in flight; split after the DMA issue */
+    /* Q: one 1 KiB DMA per head row (coalesced), operands built after the
+     * first chunk's barrier */
     const uint32_t g = mrow & 7u;
-    const float *qh = it.q + (size_t)(g < gqa ? g : 0u) * 256u;
-    h8_t qa[8];
-    {
-        fv2 qv[8][4];
-#pragma unroll
-        for (uint32_t b = 0; b < 8u; b++)
-#pragma unroll
-            for (uint32_t k = 0; k < 4u; k++)
-                qv[b][k] = ldg((const fv2 *)(qh + 32u * b + q8_kdim(b, jg, 2u * k)));
-        const float qs = g < gqa ? 1.f : 0.f;
-#pragma unroll
-        for (uint32_t b = 0; b < 8u; b++)
-#pragma unroll
-            for (uint32_t k = 0; k < 4u; k++) {
-                qa[b][2u * k] = split_hl(qv[b][k][0] * qs, lo_row);
-                qa[b][2u * k + 1u] = split_hl(qv[b][k][1] * qs, lo_row);
-            }
+    if ((((uintptr_t)it.q) & 15u) == 0) {
+        for (uint32_t h = wave; h < gqa; h += 4u)
+            dma16(it.q + (size_t)h * 256u + 4u * lane, qraw + h * 260u);
+    } else {
+        for (uint32_t e = tid; e < gqa * 256u; e += 256u)
+            qraw[(e >> 8) * 260u + (e & 255u)] = ldg(it.q + e);
     }
-
+    h8_t qa[8];
+    TRACE(1);
     float m_run[4], l_run[4];
     f4_t acc[4];
 #pragma unroll
@@ -770,8 +764,22 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
                 *(uint16_t *)(vraw + r * ROWB + q * 2u) = ldg((const uint16_t *)(vbase + off));
             }
         }
+        TRACE(2);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        TRACE(3);
+        if (c == c0) {
+            const float *qr = qraw + (g < gqa ? g : 0u) * 260u;
+            const float qs = g < gqa ? 1.f : 0.f;
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++)
+#pragma unroll
+                for (uint32_t kk = 0; kk < 4u; kk++) {
+                    const fv2 v = *(const fv2 *)(qr + 32u * b + q8_kdim(b, jg, 2u * kk));
+                    qa[b][2u * kk] = split_hl(v[0] * qs, lo_row);
+                    qa[b][2u * kk + 1u] = split_hl(v[1] * qs, lo_row);
+                }
+        }
         if (c + 1u < c1) {
 #pragma unroll
             for (uint32_t u = 0; u <= NLD; u++) jcur[u] += CP;
@@ -795,6 +803,7 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
                 qa[b], kb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             S += ks * C;
         }
+        TRACE(4);
         const bool valid = s_pos[r] >= 0;
         float T[4];
 #pragma unroll
@@ -803,7 +812,9 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
             const float cm = row16_max(T[i]);
             if (mrow == 0 && jg < 2u) s_cmax[wave][4u * jg + i] = cm;
         }
+        TRACE(5);
         __syncthreads();
+        TRACE(6);
         float alpha[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
@@ -818,7 +829,9 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
             const float ps = row16_sum(w);
             if (mrow == 0 && jg < 2u) s_psum[wave][4u * jg + i] = ps;
         }
+        TRACE(7);
         __syncthreads();
+        TRACE(8);
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
             const uint32_t h = (4u * jg + i) & 7u;
@@ -859,7 +872,9 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
                     A, h8_minus_1152(r1), acc[2u * u + 1u], 0, 0, 0);
             }
         }
+        TRACE(9);
         __syncthreads();
+        TRACE(10);
     }
 
     /* ---- epilogue: hi+lo rows -> LDS [head][col], then 16-byte stores ---- */
@@ -880,6 +895,7 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
         }
     }
     __syncthreads();
+    TRACE(11);
     if (a.S == 1u) {
         /* thread -> (head, 8 consecutive dims) */
 #pragma unroll
@@ -917,6 +933,7 @@ __global__ __launch_bounds__(256) void qsa_q8d256_k(AttnArgs a) {
             stg((fv2 *)(pbase + tid * PSTRIDE), (fv2){s_ml[0][tid], s_ml[1][tid]});
         }
     }
+    TRACE(12);
 }
 
 /* Merge the S split partials of one (item, head): weights 2^(m_s - M) over
@@ -1023,13 +1040,16 @@ static inline bool prof_armed(void) {
     return g_prof_on && !q4kv_capturing && g_prof_n < g_prof_max;
 }
 
-#define Q4KV_TARGET_WG 2048u /* aim for >= 8 workgroups per CU */
+#define Q4KV_TARGET_WG 512u /* two resident workgroups per CU */
 #define Q4KV_MAX_GRID_Y 65535u
 
 template <int KIND, int MODE>
 static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa) {
     constexpr uint32_t CP = KCfg<KIND>::CP;
     const uint32_t n_chunks = (max_n + CP - 1u) / CP;
+    /* Fill the chip once: the fast q8 kernel keeps 2 workgroups per CU
+     * resident, the generic one about as many; more splits than that only
+     * add a second round of workgroups and more partials to merge. */
     uint32_t S = (Q4KV_TARGET_WG + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
