@@ -296,3 +296,67 @@ def test_graph_captured_append_and_decode_replays(rt, oracle):
         assert np.array_equal(rt.download(kc, hk.size), hk)
     finally:
         rt.lib.q4_hip_graph_free(g)
+
+
+# ------------------------------------------------- config 4 widths at full length
+@pytest.mark.parametrize("kind", [1, 0])
+def test_config4_widths_sparse_decode_262k(rt, oracle, kind):
+    note(f"config4 width kind={kind} at 262144")
+    rng = np.random.default_rng(1239 + kind)
+    n_head, n_kvh, hd, ctx = 16, 2, 256, 262144
+    k, v = heads(rng, (ctx, n_kvh)), heads(rng, (ctx, n_kvh))
+    q = heads(rng, (1, n_head))
+    kc, _ = quantize_on_gpu(rt, k, kind)
+    vc, _ = quantize_on_gpu(rt, v, kind)
+    sel = np.stack([selection(rng, ctx - 1) for _ in range(n_kvh)])
+    got = gpu_idx_kv(rt, q, kc, vc, kind, n_head, n_kvh, hd, sel.ravel(), WIDTH,
+                     n_kvh * WIDTH, WIDTH, ctx)
+    rt.free(kc)
+    rt.free(vc)
+    want = oracle.attn(q, oracle.encode(k, kind), oracle.encode(v, kind), kind, n_head,
+                       n_kvh, hd, 1, idx=sel.ravel(), width=WIDTH, tok_stride=n_kvh * WIDTH,
+                       kvh_stride=WIDTH, max_kv=ctx)
+    assert_attn_close(got, want, what=f"width {kind}")
+
+
+# ------------------------------------------------- config 3: chunked prefill
+def test_config3_chunked_prefill_sampled(rt, oracle):
+    """16384-token q8_0 cache + an 8192-token fp32 chunk quantised and appended,
+    then causal QSA attention for every query of the chunk over its own
+    selection (3 sinks + 512 recent causal + up to 1536 uniform earlier). All
+    8192 queries run on the GPU; 64 sampled queries are checked against the
+    oracle, and the appended chunk's bytes are checked in full."""
+    note("config3 prefill 8192 after 16384")
+    rng = np.random.default_rng(1237)
+    n_head, n_kvh, hd, base, n_tok = 16, 2, 256, 16384, 8192
+    ctx = base + n_tok
+    k, v = heads(rng, (ctx, n_kvh)), heads(rng, (ctx, n_kvh))
+    q = heads(rng, (n_tok, n_head))
+    bpt = q4kv.token_bytes(2, n_kvh, hd)
+    kc, vc = rt.alloc(ctx * bpt), rt.alloc(ctx * bpt)
+    for cache, x in ((kc, k), (vc, v)):
+        src = rt.upload(x[:base])
+        assert rt.lib.q4_hip_f32_to_q8(cache, src, base * n_kvh * hd)
+        chunk = rt.upload(x[base:])
+        assert rt.lib.q4_hip_f32_to_q8(cache + base * bpt, chunk, n_tok * n_kvh * hd)
+        rt.sync()
+        rt.free(src)
+        rt.free(chunk)
+    sel = np.empty((n_tok, n_kvh, WIDTH), np.int32)
+    for t in range(n_tok):
+        for kh in range(n_kvh):
+            sel[t, kh] = selection(rng, base + t)
+    got = gpu_idx_kv(rt, q, kc, vc, 2, n_head, n_kvh, hd, sel.ravel(), WIDTH, n_kvh * WIDTH,
+                     WIDTH, ctx)
+    kb, vb = oracle.quant_q8(k), oracle.quant_q8(v)
+    assert np.array_equal(rt.download(kc, kb.size), kb)
+    assert np.array_equal(rt.download(vc, vb.size), vb)
+    rt.free(kc)
+    rt.free(vc)
+    ts = np.sort(rng.choice(n_tok, 64, replace=False))
+    ts[0], ts[-1] = 0, n_tok - 1
+    want = oracle.attn(q[ts], kb, vb, 2, n_head, n_kvh, hd, len(ts), idx=sel[ts].ravel(),
+                       width=WIDTH, tok_stride=n_kvh * WIDTH, kvh_stride=WIDTH, max_kv=ctx,
+                       threads=8)
+    assert_attn_close(got[ts], want, what="config3 sampled queries")
+    assert np.all(np.isfinite(got))
