@@ -65,10 +65,13 @@ class Bench:
         self.L, self.R = layers, sets
         self.rt = rt = q4kv.Runtime()
         self.lib = lib = rt.lib
-        synth = C.CDLL(str(PKG / "lib" / "libq4kv_synth.so"))
+        self.synth = synth = C.CDLL(str(PKG / "lib" / "libq4kv_synth.so"))
         synth.q4kv_synth_heads.restype = C.c_int
         synth.q4kv_synth_heads.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint64,
                                            C.c_int, C.c_int, C.c_int, C.c_int]
+        synth.q4kv_gather_probe_us.restype = C.c_double
+        synth.q4kv_gather_probe_us.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32,
+                                               C.c_uint32, C.c_uint32, C.c_uint32, C.c_int]
 
         def gen(ptr, n, seed):
             assert synth.q4kv_synth_heads(ptr, n, HD, seed, *OUTLIERS) == 0
@@ -183,6 +186,21 @@ class Bench:
             kern = tot.value / n if n > 0 else None
         return wall, gpu_ms / 1e3, kern
 
+    def gather_ceiling(self, iters=400):
+        """The same rows the batched step gathers, DMA'd with no compute: the
+        practical roofline of this access pattern on this GPU."""
+        n = self.R * self.L
+        kc = (C.c_void_p * n)(*[self.kc[i % self.L] for i in range(n)])
+        vc = (C.c_void_p * n)(*[self.vc[i % self.L] for i in range(n)])
+        ix = (C.c_void_p * n)(*[self.sel_ptr(i // self.L, i % self.L) for i in range(n)])
+        d = [self.rt.alloc(8 * n) for _ in range(3)]
+        for dp, arr in zip(d, (kc, vc, ix)):
+            assert self.lib.q4_hip_h2d(dp, C.addressof(arr), 8 * n)
+        self.rt.sync()
+        us = self.synth.q4kv_gather_probe_us(d[0], d[1], d[2], self.L, self.R, N_KVH, WIDTH,
+                                             iters)
+        return us, self.L * GATHER_B / (us * 1e-6) / 1e9
+
     # ---- parity of the last batched step vs the oracle (layer 0) ------------
     def check_and_cpu(self, cpu_seconds, threads):
         from oracle_ffi import Oracle
@@ -262,17 +280,29 @@ def main():
     ap.add_argument("--sets", type=int, default=16)
     ap.add_argument("--mode", choices=["batched", "sequential", "both"], default="both")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a device-to-device copy of MIB MiB (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the QSA KV path runs on a single MI355X "
               "(no collectives); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        rt = q4kv.Runtime()
+        n = args.copy_calibration << 20
+        src, dst = rt.alloc(n), rt.alloc(n)
+        for _ in range(3):
+            assert rt.lib.q4_hip_copy(dst, src, n // 4)
+        rt.sync()
+        print(json.dumps({"copy_bytes": n, "launches": 3}))
+        return
     b = Bench(args.layers, args.sets)
     res = {}
     if args.mode in ("batched", "both"):
         res["batched"] = b.timed(b.step_batched, args.steps, args.warmup, prof=True)
     if args.mode in ("sequential", "both"):
         res["sequential"] = b.timed(b.step_sequential, args.steps, args.warmup)
+    g_us, g_gbs = b.gather_ceiling()
     threads = min(16, os.cpu_count() or 1)
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
     head = "batched" if "batched" in res else "sequential"
@@ -302,9 +332,20 @@ def main():
         ach = L * SPLIT_KERNEL_B / (kern_s / 1e3) / 1e9
         out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS,
                            "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4), "traffic": None,
-                           "kernel": "qsa_attn_k<q8,batch>",
+                           "kernel": "qsa_q8d256_k<MODE_BATCH>",
                            "kernel_us": round(kern_s * 1e3, 3),
                            "bytes_per_launch": L * SPLIT_KERNEL_B}
+    out["gather_ceiling"] = {
+        "gbs": round(g_gbs, 1), "us_per_launch": round(g_us, 3),
+        "what": "the same K/V rows of one batched step DMA'd to LDS with no compute "
+                "(272-byte rows, 16-byte loads): the practical bound of this access pattern"}
+    tfile = ROOT / "profiles" / "qsa_q8d256_batch12_traffic.json"
+    if kern_s and tfile.exists() and L == 12:
+        t = json.loads(tfile.read_text())
+        out["roofline"]["traffic"] = t["hbm_bytes_per_launch"]
+        out["roofline"]["traffic_source"] = str(tfile.relative_to(ROOT))
+    if kern_s:
+        out["roofline"]["frac_of_gather_ceiling"] = round(out["roofline"]["achieved"] / g_gbs, 4)
     out.update(parity)
     out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)

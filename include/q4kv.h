@@ -138,6 +138,10 @@ typedef struct {
 bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc, uint32_t n,
                             uint32_t bpt, int kind);
 
+/* Run all library work on the caller's HIP stream (an engine's own compute
+ * stream), or on the library's stream again when stream is NULL. */
+bool q4kv_use_stream(void *stream);
+
 /* Pinned host buffers for restoring a session KV image (hipHostMalloc). */
 void *q4_hip_host_alloc(size_t n);
 void q4_hip_host_free(void *p);

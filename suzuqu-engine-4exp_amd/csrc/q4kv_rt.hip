@@ -24,7 +24,15 @@ int32_t *q4kv_pos_d = nullptr;
 float *q4kv_part = nullptr;
 size_t q4kv_part_cap = 0;
 
-static int32_t *g_pos_h = nullptr; /* pinned staging for position pushes */
+/* Pinned staging ring for position pushes: a slot is rewritten only after the
+ * copy that last read it has completed (its event), so pushes never block on
+ * the whole stream. */
+#define POS_SLOTS 16
+static int32_t *g_pos_h = nullptr;
+static hipEvent_t g_pos_ev[POS_SLOTS];
+static int g_pos_used[POS_SLOTS];
+static unsigned g_pos_next = 0;
+static hipStream_t g_own_stream = nullptr; /* the stream q4_hip_init created */
 static uint32_t g_last_graph_nodes = 0;
 
 /* Split-KV partials: 8M floats (32 MiB) covers e.g. 64 sequences x 2 KV
@@ -57,11 +65,17 @@ extern "C" bool q4_hip_init(void) {
         (void)hipGetLastError();
         return false;
     }
+    g_own_stream = q4kv_stream;
     if (hipMalloc((void **)&q4kv_pos_d, sizeof(int32_t)) != hipSuccess ||
-        hipHostMalloc((void **)&g_pos_h, sizeof(int32_t), hipHostMallocDefault) !=
+        hipHostMalloc((void **)&g_pos_h, POS_SLOTS * sizeof(int32_t), hipHostMallocDefault) !=
             hipSuccess) {
         (void)hipGetLastError();
         return false;
+    }
+    for (int i = 0; i < POS_SLOTS; i++) {
+        if (hipEventCreateWithFlags(&g_pos_ev[i], hipEventDisableTiming) != hipSuccess)
+            return false;
+        g_pos_used[i] = 0;
     }
     *g_pos_h = 0;
     if (hipMemcpy(q4kv_pos_d, g_pos_h, sizeof(int32_t), hipMemcpyHostToDevice) !=
@@ -85,7 +99,9 @@ extern "C" void q4_hip_shutdown(void) {
     if (q4kv_part) (void)hipFree(q4kv_part);
     if (q4kv_pos_d) (void)hipFree(q4kv_pos_d);
     if (g_pos_h) (void)hipHostFree(g_pos_h);
-    (void)hipStreamDestroy(q4kv_stream);
+    for (int i = 0; i < POS_SLOTS; i++) (void)hipEventDestroy(g_pos_ev[i]);
+    (void)hipStreamDestroy(g_own_stream);
+    g_own_stream = nullptr;
     q4kv_part = nullptr;
     q4kv_part_cap = 0;
     q4kv_pos_d = nullptr;
@@ -95,6 +111,16 @@ extern "C" void q4_hip_shutdown(void) {
 }
 
 extern "C" bool q4_hip_ok(void) { return q4kv_ok != 0; }
+
+/* Enqueue all library work on the caller's stream (e.g. the engine's
+ * compute stream, so its producers and these kernels stay ordered); NULL
+ * returns to the library's own stream. Not while capturing. */
+extern "C" bool q4kv_use_stream(void *stream) {
+    if (!q4kv_ok || q4kv_capturing) return false;
+    (void)hipStreamSynchronize(q4kv_stream);
+    q4kv_stream = stream ? (hipStream_t)stream : g_own_stream;
+    return true;
+}
 
 extern "C" void *q4_hip_malloc(size_t n) {
     if (!q4kv_ok || n == 0) return nullptr;
@@ -170,11 +196,15 @@ extern "C" void q4_hip_host_free(void *p) {
 /* ---- device decode position (src/q4_rocm.cu:6218-6227) ---- */
 extern "C" void q4_hip_pos_push(int32_t pos) {
     if (!q4kv_pos_d || !g_pos_h || !q4kv_stream) return;
-    /* The pinned word may still be in flight from the previous push. */
-    if (!q4kv_capturing) (void)hipStreamSynchronize(q4kv_stream);
-    *g_pos_h = pos;
-    (void)hipMemcpyAsync(q4kv_pos_d, g_pos_h, sizeof(int32_t), hipMemcpyHostToDevice,
+    const unsigned i = g_pos_next++ % POS_SLOTS;
+    if (g_pos_used[i] && !q4kv_capturing) (void)hipEventSynchronize(g_pos_ev[i]);
+    g_pos_h[i] = pos;
+    (void)hipMemcpyAsync(q4kv_pos_d, g_pos_h + i, sizeof(int32_t), hipMemcpyHostToDevice,
                          q4kv_stream);
+    if (!q4kv_capturing) {
+        (void)hipEventRecord(g_pos_ev[i], q4kv_stream);
+        g_pos_used[i] = 1;
+    }
 }
 extern "C" int q4_hip_capturing(void) { return q4kv_capturing; }
 extern "C" int q4_hip_pos_dev_ok(void) { return q4kv_pos_d != nullptr && g_pos_h != nullptr; }

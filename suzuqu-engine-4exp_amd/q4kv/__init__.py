@@ -95,6 +95,7 @@ SIGNATURES = {
     "q4kv_timer_end_ms": (C.c_double, [C.c_int]),
     "q4kv_device_info": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_int),
                                    C.POINTER(C.c_int)]),
+    "q4kv_use_stream": (_b, [_vp]),
     "q4kv_prof_begin": (_b, [C.c_int]),
     "q4kv_prof_end": (C.c_int, [C.POINTER(C.c_double)]),
     "q4_hip_kv_append_batch": (_b, [_vp, _u32, _u32, _u32, C.c_int]),

@@ -104,3 +104,29 @@ def test_kv_append_at_device_position(rt, oracle, kind):
     rt.sync()
     assert np.array_equal(rt.download(kc, max_kv * bpt), hk)
     assert np.array_equal(rt.download(vc, max_kv * bpt), hv)
+
+
+def test_use_stream_roundtrip_keeps_ordering(rt, oracle):
+    """q4kv_use_stream(NULL) returns the library to its own stream; pushes of
+    the device position keep their order across the pinned staging ring."""
+    assert rt.lib.q4kv_use_stream(None)
+    n_kvh, hd, max_kv = 2, 256, 40
+    bpt = q4kv.token_bytes(2, n_kvh, hd)
+    kc, vc = rt.alloc(max_kv * bpt), rt.alloc(max_kv * bpt)
+    rt.h2d(kc, np.zeros(max_kv * bpt, np.uint8))
+    rt.h2d(vc, np.zeros(max_kv * bpt, np.uint8))
+    rng = np.random.default_rng(31)
+    hk = np.zeros(max_kv * bpt, np.uint8)
+    hv = np.zeros(max_kv * bpt, np.uint8)
+    rows = heads(rng, (max_kv, 2, n_kvh))
+    dr = rt.upload(rows)
+    for pos in range(max_kv):  # more pushes than staging slots, no sync between
+        rt.lib.q4_hip_pos_push(pos)
+        base = dr + pos * 2 * n_kvh * hd * 4
+        assert rt.lib.q4_hip_kv_append_d(kc, vc, base, base + n_kvh * hd * 4, n_kvh * hd,
+                                          bpt, 2)
+        oracle.lib.orc_kv_append(hk.ctypes.data, hv.ctypes.data, rows[pos, 0].ctypes.data,
+                                 rows[pos, 1].ctypes.data, n_kvh * hd, bpt, 2, pos)
+    rt.sync()
+    assert np.array_equal(rt.download(kc, hk.size), hk)
+    assert np.array_equal(rt.download(vc, hv.size), hv)
