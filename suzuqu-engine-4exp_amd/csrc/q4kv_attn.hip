@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <math.h>
+#include <stdlib.h>
 
 #include "q4kv_internal.h"
 
@@ -1040,7 +1041,17 @@ static inline bool prof_armed(void) {
     return g_prof_on && !q4kv_capturing && g_prof_n < g_prof_max;
 }
 
-#define Q4KV_TARGET_WG 512u /* two resident workgroups per CU */
+/* Workgroups a launch aims for (Q4KV_SPLIT_TARGET overrides, like the
+ * reference's Q4_DEC_SPLIT_S tuning knob). */
+static uint32_t split_target(void) {
+    static uint32_t t = 0;
+    if (!t) {
+        const char *e = getenv("Q4KV_SPLIT_TARGET");
+        const long v = e ? strtol(e, nullptr, 10) : 0;
+        t = (v >= 1 && v <= 1 << 20) ? (uint32_t)v : 512u;
+    }
+    return t;
+}
 #define Q4KV_MAX_GRID_Y 65535u
 
 template <int KIND, int MODE>
@@ -1050,7 +1061,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
     /* Fill the chip once: the fast q8 kernel keeps 2 workgroups per CU
      * resident, the generic one about as many; more splits than that only
      * add a second round of workgroups and more partials to merge. */
-    uint32_t S = (Q4KV_TARGET_WG + n_items - 1u) / n_items;
+    uint32_t S = (split_target() + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
     if (S > COMB_MAXS) S = COMB_MAXS;
