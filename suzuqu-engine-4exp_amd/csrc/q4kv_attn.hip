@@ -65,6 +65,10 @@ struct Item {
     float *out;
     const int32_t *list;
     uint32_t n, max_kv;
+    /* index-load source and mask: (list, ~0) for a list, (any readable word,
+     * 0) for a dense item, so that loads and selects need no branch */
+    const int32_t *lsrc;
+    uint32_t lmask;
 };
 
 template <int MODE>
@@ -86,6 +90,8 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
         it.max_kv = ldg(&d->max_kv);
         it.list = idx ? idx + (size_t)kh * ldg(&d->idx_kvh_stride) : nullptr;
         it.n = idx ? n_sel : (n_sel < it.max_kv ? n_sel : it.max_kv);
+        it.lsrc = idx ? it.list : (const int32_t *)a.seqs;
+        it.lmask = idx ? ~0u : 0u;
     } else {
         const size_t qo = (size_t)t * a.n_head * a.hd + hoff;
         it.kc = a.kc;
@@ -97,10 +103,14 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
         if (MODE == MODE_INDEXED) {
             it.list = a.idx + t * a.tok_stride + kh * a.kvh_stride;
             it.n = a.width;
+            it.lsrc = it.list;
+            it.lmask = ~0u;
         } else {
             const uint32_t nkv = a.kv_base + t + 1u;
             it.list = nullptr;
             it.n = nkv < a.max_kv ? nkv : a.max_kv;
+            it.lsrc = nullptr;
+            it.lmask = 0u;
         }
     }
     return it;
@@ -113,6 +123,18 @@ __device__ static inline float xor32(float v) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
                                               false);
     return __uint_as_float((threadIdx.x & 32u) ? r[0] : r[1]);
+}
+/* v + (value of the lane 32 apart): the swap leaves each lane's own value in
+ * one result and its partner's in the other, so their sum needs no select. */
+__device__ static inline float pair32_sum(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                              false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+/* max(a, b) for non-NaN operands in one v_med3_f32 (fmaxf adds NaN-quieting
+ * canonicalisations of both operands). */
+__device__ static inline float fmax2(float a, float b) {
+    return __builtin_amdgcn_fmed3f(a, b, INFINITY);
 }
 
 __device__ static inline float wave_max(float v) {
@@ -171,6 +193,13 @@ __device__ static inline float ld_f16(const uint8_t *p) {
     return __half2float(__ushort_as_half(*(const uint16_t *)p));
 }
 
+/* x -> fp16 hi part (nsel = 0) or fp16 residual x - hi (nsel = -1) without a
+ * select: one conversion and one mixed-precision FMA (v_fma_mix). */
+__device__ static inline _Float16 split_sel(float x, float nsel) {
+    const _Float16 h = (_Float16)x;
+    return (_Float16)__builtin_fmaf(nsel, (float)h, x);
+}
+
 /* x -> fp16 hi part (rows < 8) or fp16 residual (rows >= 8). */
 __device__ static inline _Float16 split_hl(float x, bool lo) {
     _Float16 h = (_Float16)x;
@@ -219,22 +248,21 @@ __device__ static inline void pos_issue(const Item &it, const uint32_t (&j)[N],
     } else {
         /* no branch on the list pointer (a branch would force a wait at its
          * merge): dense batch items load a harmless word and keep j */
-        const bool has = MODE == MODE_INDEXED || it.list != nullptr;
+        const uint32_t m = MODE == MODE_INDEXED ? ~0u : it.lmask;
 #pragma unroll
         for (int u = 0; u < N; u++) {
-            const int32_t *src = has ? it.list + (j[u] < it.n ? j[u] : it.n - 1u)
-                                     : (const int32_t *)it.q;
-            raw[u] = *(const GLOBAL int32_t *)src;
+            const uint32_t jj = (j[u] < it.n ? j[u] : it.n - 1u) & m;
+            raw[u] = *(const GLOBAL int32_t *)(it.lsrc + jj);
         }
     }
 }
 template <int N, int MODE>
 __device__ static inline void pos_finish(const Item &it, const uint32_t (&j)[N],
                                          const int32_t (&raw)[N], int32_t (&p)[N]) {
-    const bool has = MODE == MODE_INDEXED || (MODE == MODE_BATCH && it.list != nullptr);
+    const uint32_t m = MODE == MODE_INDEXED ? ~0u : (MODE == MODE_BATCH ? it.lmask : 0u);
 #pragma unroll
     for (int u = 0; u < N; u++) {
-        const int32_t r = has ? raw[u] : (int32_t)j[u];
+        const int32_t r = (int32_t)(((uint32_t)raw[u] & m) | (j[u] & ~m));
         p[u] = (j[u] < it.n && r >= 0 && (uint32_t)r < it.max_kv) ? r : -1;
     }
 }
@@ -249,13 +277,13 @@ __device__ static inline void dma16(const void *src, void *lds_wave_base) {
 
 /* Reductions over the 16 lanes of a DPP row (one MFMA column group). */
 template <int CTRL> __device__ static inline float dppf(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 __device__ static inline float row16_max(float v) {
-    v = fmaxf(v, dppf<0xB1>(v));  /* quad_perm [1,0,3,2] */
-    v = fmaxf(v, dppf<0x4E>(v));  /* quad_perm [2,3,0,1] */
-    v = fmaxf(v, dppf<0x141>(v)); /* row_half_mirror */
-    return fmaxf(v, dppf<0x140>(v)); /* row_mirror */
+    v = fmax2(v, dppf<0xB1>(v));  /* quad_perm [1,0,3,2] */
+    v = fmax2(v, dppf<0x4E>(v));  /* quad_perm [2,3,0,1] */
+    v = fmax2(v, dppf<0x141>(v)); /* row_half_mirror */
+    return fmax2(v, dppf<0x140>(v)); /* row_mirror */
 }
 __device__ static inline float row16_sum(float v) {
     v += dppf<0xB1>(v);
@@ -677,13 +705,20 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
     TRACE(10);
 }
 
+/* MFMA output column (fast kernel tile order) holding head dimension d. */
+__device__ static inline uint32_t q8_col_of_dim(uint32_t d) {
+    const uint32_t bb = d >> 5, w = bb >> 1;
+    const uint32_t t = 2u * (bb & 1u) + (d & 1u), n = (d & 31u) >> 1;
+    return (w * 4u + t) * 16u + n;
+}
+
 /* Fast path for the production shape: q8_0 cache, head_dim 256 (272-byte
  * rows, 17 x 16 B), at most 8 query heads per KV head. Same algorithm as
  * qsa_attn_k with every shape constant compile-time, the weight hi/lo split
  * done with mixed-precision FMAs, and the partial / output rows staged
  * through LDS for 16-byte stores. */
 template <int MODE>
-__global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     constexpr uint32_t CP = 64, ROWB = 272, NCH = 17, NLD = 5;
     __shared__ __attribute__((aligned(16))) uint8_t kraw[CP * ROWB];
     __shared__ __attribute__((aligned(16))) uint8_t vraw[CP * ROWB];
@@ -707,6 +742,11 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
     const uint32_t mrow = lane & 15u, jg = lane >> 4;
     const bool lo_row = mrow >= 8u;
     const size_t rstride = (size_t)a.n_kvh * ROWB; /* bytes per token */
+    /* even q8_0 blocks: byte offset of this lane's first dword in the block
+     * pair, and the perm selector of its second (identity except group 3) */
+    const uint32_t k_eoff = jg < 3u ? 4u + 8u * jg : 28u;
+    const float nsel = lo_row ? -1.f : 0.f;
+    const uint32_t k_esel = jg == 3u ? 0x05040302u : 0x07060504u;
     const uint8_t *kbase = it.kc + (size_t)kh * ROWB, *vbase = it.vc + (size_t)kh * ROWB;
 
     /* rows this lane DMAs (u < 4 always valid, u = 4 only in wave 0) and the
@@ -777,8 +817,8 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
 #pragma unroll
                 for (uint32_t kk = 0; kk < 4u; kk++) {
                     const fv2 v = *(const fv2 *)(qr + 32u * b + q8_kdim(b, jg, 2u * kk));
-                    qa[b][2u * kk] = split_hl(v[0] * qs, lo_row);
-                    qa[b][2u * kk + 1u] = split_hl(v[1] * qs, lo_row);
+                    qa[b][2u * kk] = split_sel(v[0] * qs, nsel);
+                    qa[b][2u * kk + 1u] = split_sel(v[1] * qs, nsel);
                 }
         }
         if (c + 1u < c1) {
@@ -790,7 +830,8 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
 #pragma unroll
         for (uint32_t k = 0; k < 2u; k++) {
             const uint32_t e = tid + 256u * k, b = e >> 6, r = e & 63u;
-            vsc[e] = s_pos[r] < 0 ? 0.f : ld_f16(vraw + r * ROWB + 34u * b);
+            const float x = ld_f16(vraw + r * ROWB + 34u * b);
+            vsc[e] = s_pos[r] < 0 ? 0.f : x;
         }
         /* ---- scores: wave w, positions 16w .. 16w+15 ---- */
         const uint32_t r = wave * 16u + mrow;
@@ -798,7 +839,22 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
         f4_t S = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (uint32_t b = 0; b < 8u; b++) {
-            const h8_t kb = load_k_q8(krow, b, jg);
+            /* k-group jg of block b: odd blocks are dword aligned; even ones
+             * take their group-3 tail from the pair's leading dword */
+            const uint8_t *pb = krow + 68u * (b >> 1);
+            uint32_t w0, w1;
+            if (b & 1u) {
+                w0 = *(const uint32_t *)(pb + 36u + 8u * jg);
+                w1 = *(const uint32_t *)(pb + 40u + 8u * jg);
+            } else {
+                w0 = *(const uint32_t *)(pb + k_eoff);
+                w1 = __builtin_amdgcn_perm(*(const uint32_t *)(pb + k_eoff + 4u),
+                                           *(const uint32_t *)pb, k_esel);
+            }
+            uint32_t r0, r1, r2, r3;
+            i8x4_to_h4(w0, r0, r1);
+            i8x4_to_h4(w1, r2, r3);
+            const h8_t kb = h8_minus_1152((u4_t){r0, r1, r2, r3});
             const float ks = ld_f16(krow + 34u * b);
             const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                 qa[b], kb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -809,7 +865,8 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
         float T[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
-            T[i] = valid ? (S[i] + xor32(S[i])) * a.scale_log2 : -INFINITY;
+            const float t = pair32_sum(S[i]) * a.scale_log2;
+            T[i] = valid ? t : -INFINITY;
             const float cm = row16_max(T[i]);
             if (mrow == 0 && jg < 2u) s_cmax[wave][4u * jg + i] = cm;
         }
@@ -820,12 +877,15 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
             const uint32_t h = (4u * jg + i) & 7u;
-            const float cm = fmaxf(fmaxf(s_cmax[0][h], s_cmax[1][h]),
-                                   fmaxf(s_cmax[2][h], s_cmax[3][h]));
-            const float mn = fmaxf(m_run[i], cm);
-            alpha[i] = m_run[i] == -INFINITY ? 0.f : exp2f(m_run[i] - mn);
+            const float cm = fmax2(fmax2(s_cmax[0][h], s_cmax[1][h]),
+                                   fmax2(s_cmax[2][h], s_cmax[3][h]));
+            const float mn = fmax2(m_run[i], cm);
+            /* exp2(-inf) = 0 handles masked scores and the first chunk; a
+             * still-empty max is shifted to 0 so that -inf - -inf is avoided */
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - ms);
             m_run[i] = mn;
-            const float w = T[i] == -INFINITY ? 0.f : exp2f(T[i] - mn);
+            const float w = __builtin_amdgcn_exp2f(T[i] - ms);
             if (lane < 32u) sw[(4u * jg + i) * CP + r] = w;
             const float ps = row16_sum(w);
             if (mrow == 0 && jg < 2u) s_psum[wave][4u * jg + i] = ps;
@@ -862,11 +922,7 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
                 const float *sp = vsc + bb * CP + p0;
                 h8_t A;
 #pragma unroll
-                for (uint32_t i = 0; i < 8u; i++) {
-                    const float x = wp[i] * sp[i];
-                    const _Float16 hi = (_Float16)x;
-                    A[i] = lo_row ? (_Float16)__builtin_fmaf(wp[i], sp[i], -(float)hi) : hi;
-                }
+                for (uint32_t i = 0; i < 8u; i++) A[i] = split_sel(wp[i] * sp[i], nsel);
                 acc[2u * u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, h8_minus_1152(r0),
                                                                     acc[2u * u], 0, 0, 0);
                 acc[2u * u + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
@@ -908,9 +964,8 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
                 f4_t o;
 #pragma unroll
                 for (uint32_t j = 0; j < 4u; j++) {
-                    const uint32_t d = d0 + j, bb = d >> 5, w = bb >> 1;
-                    const uint32_t t = 2u * (bb & 1u) + (d & 1u), n = (d & 31u) >> 1;
-                    float rv = so[h * 256u + (w * 4u + t) * 16u + n] * inv;
+                    const uint32_t d = d0 + j;
+                    float rv = so[h * 256u + q8_col_of_dim(d)] * inv;
                     if (it.gate) rv *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)h * 256u + d)));
                     o[j] = rv;
                 }
@@ -939,67 +994,80 @@ __global__ __launch_bounds__(256, 3) void qsa_q8d256_k(AttnArgs a) {
 
 /* Merge the S split partials of one (item, head): weights 2^(m_s - M) over
  * splits with l_s > 0, then the sigmoid gate (src/q4_rocm.cu:6968-7013).
- * Thread c owns output column c; for S <= 64 every partial load is issued
- * up front, so the merge costs one memory round trip. */
+ * Thread c owns output column c. For S <= COMB_REG every partial load
+ * (columns and the wave-uniform m_s, l_s) is issued before the first is used
+ * and the merge needs neither LDS nor barriers: one memory round trip. */
 #define COMB_MAXS 1024u
 #define COMB_REG 64u
+
+/* R >= S: all S partials in registers (indices past S re-read split S-1 and
+ * get weight 0). */
+template <uint32_t R>
+__device__ static inline float comb_reg(const float *pb, size_t sst, uint32_t S, uint32_t col,
+                                        float &L) {
+    float v[R], m[R], l[R];
+    /* a per-lane zero the compiler cannot fold: keeps the uniform m_s, l_s
+     * loads on the vector path, issued with the column loads (scalar loads
+     * would be waited for in small groups) */
+    uint32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+#pragma unroll
+    for (uint32_t k = 0; k < R; k++) {
+        const float *p = pb + (k < S ? k : S - 1u) * sst;
+        m[k] = ldg(p + z);
+        l[k] = ldg(p + 1u + z);
+        v[k] = ldg(p + 2u + col);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (uint32_t k = 0; k < R; k++)
+        if (k < S && l[k] > 0.f) M = fmax2(M, m[k]);
+    float acc = 0.f;
+    L = 0.f;
+#pragma unroll
+    for (uint32_t k = 0; k < R; k++) {
+        const float e = __builtin_amdgcn_exp2f(m[k] - M);
+        const float w = (k < S && l[k] > 0.f) ? e : 0.f;
+        L += w * l[k];
+        acc += w * v[k];
+    }
+    return acc;
+}
+
 template <int KIND, int MODE>
 __global__ __launch_bounds__(256) void qsa_comb_k(AttnArgs a) {
-    __shared__ float wsh[COMB_MAXS];
-    __shared__ float red[2][4];
     const uint32_t g = blockIdx.x, item = a.item0 + blockIdx.y, tid = threadIdx.x;
     const uint32_t gqa = a.n_head / a.n_kvh, hd = a.hd, S = a.S;
-    const uint32_t lane = tid & 63u, wave = tid >> 6;
-    const Item it = resolve_item<MODE>(a, item);
     const float *pb = a.part + ((size_t)item * S * gqa + g) * PSTRIDE;
     const size_t sst = (size_t)gqa * PSTRIDE;
     const uint32_t dim = col_dim<KIND>(tid);
     const bool dvalid = dim < hd;
-    float gate = 1.f;
-    if (it.gate && dvalid) gate = 1.f / (1.f + expf(-ldg(it.gate + (size_t)g * hd + dim)));
-    float v[COMB_REG];
-    if (S <= COMB_REG) {
-#pragma unroll
-        for (uint32_t k = 0; k < COMB_REG; k++)
-            v[k] = (k < S && dvalid) ? ldg(pb + k * sst + 2u + tid) : 0.f;
+    const uint32_t col = dvalid ? tid : 0u;
+    float L = 0.f, acc = 0.f;
+    if (S <= 8u) acc = comb_reg<8>(pb, sst, S, col, L);
+    else if (S <= 16u) acc = comb_reg<16>(pb, sst, S, col, L);
+    else if (S <= 24u) acc = comb_reg<24>(pb, sst, S, col, L);
+    else if (S <= 32u) acc = comb_reg<32>(pb, sst, S, col, L);
+    else if (S <= 48u) acc = comb_reg<48>(pb, sst, S, col, L);
+    else if (S <= COMB_REG) acc = comb_reg<COMB_REG>(pb, sst, S, col, L);
+    else {
+        /* long split lists: two passes over the partials */
+        float M = -INFINITY;
+        for (uint32_t sp = 0; sp < S; sp++)
+            if (ldg(pb + sp * sst + 1u) > 0.f) M = fmax2(M, ldg(pb + sp * sst));
+        for (uint32_t sp = 0; sp < S; sp++) {
+            const float l = ldg(pb + sp * sst + 1u);
+            if (l > 0.f) {
+                const float w = __builtin_amdgcn_exp2f(ldg(pb + sp * sst) - M);
+                L += w * l;
+                acc += w * ldg(pb + sp * sst + 2u + col);
+            }
+        }
     }
-    float mloc[COMB_MAXS / 256u], lloc[COMB_MAXS / 256u];
-    float M = -INFINITY;
-#pragma unroll
-    for (uint32_t k = 0; k < COMB_MAXS / 256u; k++) {
-        const uint32_t sp = tid + 256u * k;
-        mloc[k] = sp < S ? ldg(pb + sp * sst) : -INFINITY;
-        lloc[k] = sp < S ? ldg(pb + sp * sst + 1u) : 0.f;
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < COMB_MAXS / 256u; k++)
-        if (lloc[k] > 0.f) M = fmaxf(M, mloc[k]);
-    M = wave_max(M);
-    if (lane == 0) red[0][wave] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    float L = 0.f;
-#pragma unroll
-    for (uint32_t k = 0; k < COMB_MAXS / 256u; k++) {
-        const uint32_t sp = tid + 256u * k;
-        const float w = lloc[k] > 0.f ? exp2f(mloc[k] - M) : 0.f;
-        if (sp < S) wsh[sp] = w;
-        L += w * lloc[k];
-    }
-    L = wave_sum(L);
-    if (lane == 0) red[1][wave] = L;
-    __syncthreads();
-    L = red[1][0] + red[1][1] + red[1][2] + red[1][3];
     if (!dvalid) return;
-    float acc = 0.f;
-    if (S <= COMB_REG) {
-#pragma unroll
-        for (uint32_t k = 0; k < COMB_REG; k++)
-            if (k < S) acc += wsh[k] * v[k];
-    } else {
-        for (uint32_t sp = 0; sp < S; sp++) acc += wsh[sp] * ldg(pb + sp * sst + 2u + tid);
-    }
-    const float r = L > 0.f ? acc / L * gate : 0.f;
+    const Item it = resolve_item<MODE>(a, item);
+    float r = L > 0.f ? acc / L : 0.f;
+    if (it.gate) r *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)g * hd + dim)));
     stg(it.out + (size_t)g * hd + dim, r);
 }
 
@@ -1061,6 +1129,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
     /* Fill the chip once: the fast q8 kernel keeps 2 workgroups per CU
      * resident, the generic one about as many; more splits than that only
      * add a second round of workgroups and more partials to merge. */
+    const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
     uint32_t S = (split_target() + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
@@ -1080,7 +1149,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         dim3 grid(S, ni);
         const bool prof = prof_armed();
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
-        if (KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u)
+        if (fast)
             qsa_q8d256_k<MODE><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (gqa <= 8u)
             qsa_attn_k<KIND, MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
