@@ -12,12 +12,14 @@ different decode positions rotate across steps so the 27 MB a step gathers
 is not served from the 256 MB Infinity Cache.
 
 Modes:
-  batched    -- all 12 layers' appends in one launch, their attention in one
-                split-KV launch + merge (headline `value`).
+  batched    -- all 12 layers' steps in one q4_hip_qsa_step_batch call: the
+                appends and the split-KV attention in one launch, then the
+                split merge (headline `value`).
   sequential -- per layer append + attention launches, captured into one
                 hipGraph per step (what a batch-1 decode executes).
 
-Prints one JSON line (see the metric contract in DESIGN.md).
+Prints one JSON line: metric, value (GB/s of algorithmic bytes), roofline of the
+fused step kernel and the CPU baseline.
 """
 from __future__ import annotations
 
@@ -49,8 +51,11 @@ GATHER_B = 2 * N_KVH * WIDTH * ROW        # K+V rows gathered per layer
 IDX_B = N_KVH * WIDTH * 4
 QO_B = N_HEAD * HD * 4
 APPEND_B = 2 * N_KVH * HD * 4 + 2 * BPT   # read fp32 K,V rows + write q8 rows
-LAYER_B = GATHER_B + IDX_B + 2 * QO_B + APPEND_B  # 2 285 848 B (SURVEY 8d)
-SPLIT_KERNEL_B = GATHER_B + IDX_B + QO_B  # what the split-KV kernel must read
+# algorithmic bytes of one layer's step: gather + lists + q in / out + append
+LAYER_B = GATHER_B + IDX_B + 2 * QO_B + APPEND_B  # 2 285 848 B
+# what the fused append + split-KV kernel must move per layer (its partials
+# stay on chip up to the merge, which is not counted here)
+SPLIT_KERNEL_B = GATHER_B + IDX_B + QO_B + APPEND_B
 
 
 def selection(rng, pos):
@@ -106,21 +111,22 @@ class Bench:
         gen(self.d_nv, self.R * self.L * N_KVH * HD, 79)
         self.d_out = rt.alloc(self.L * N_HEAD * HD * 4)
         seq = (q4kv.SeqDesc * (self.R * self.L))()
-        app = (q4kv.AppendDesc * (self.R * self.L))()
+        step = (q4kv.StepDesc * (self.R * self.L))()
         for s in range(self.R):
             for layer in range(self.L):
                 i = s * self.L + layer
                 seq[i] = q4kv.SeqDesc(self.kc[layer], self.vc[layer], self.q_ptr(s, layer),
                                       None, self.d_out + layer * QO_B,
                                       self.sel_ptr(s, layer), WIDTH, WIDTH, CTX, 0)
-                app[i] = q4kv.AppendDesc(self.kc[layer], self.vc[layer],
-                                         self.row_ptr(self.d_nk, s, layer),
-                                         self.row_ptr(self.d_nv, s, layer), self.pos[s], 0)
+                step[i] = q4kv.StepDesc(seq[i], self.row_ptr(self.d_nk, s, layer),
+                                        self.row_ptr(self.d_nv, s, layer), self.pos[s])
         self.d_seq = rt.alloc(C.sizeof(seq))
-        self.d_app = rt.alloc(C.sizeof(app))
+        self.d_step = rt.alloc(C.sizeof(step))
         assert lib.q4_hip_h2d(self.d_seq, C.addressof(seq), C.sizeof(seq))
-        assert lib.q4_hip_h2d(self.d_app, C.addressof(app), C.sizeof(app))
+        assert lib.q4_hip_h2d(self.d_step, C.addressof(step), C.sizeof(step))
         self.graphs = None
+        self.bgraphs = None
+        self.pad = None
 
     def q_ptr(self, s, layer):
         return self.d_q + (s * self.L + layer) * QO_B
@@ -132,13 +138,47 @@ class Bench:
         return base + (s * self.L + layer) * N_KVH * HD * 4
 
     # ---- one step -----------------------------------------------------------
+    def _enqueue_batched(self, s):
+        return self.lib.q4_hip_qsa_step_batch(
+            self.d_step + s * self.L * C.sizeof(q4kv.StepDesc), self.L, N_HEAD, N_KVH, HD,
+            1.0 / 16, q4kv.KV_Q8, WIDTH)
+
     def step_batched(self, s):
-        lib = self.lib
-        ok = lib.q4_hip_kv_append_batch(self.d_app + s * self.L * C.sizeof(q4kv.AppendDesc),
-                                        self.L, N_KVH * HD, BPT, q4kv.KV_Q8)
-        ok = ok and lib.q4_hip_qsa_decode_batch(self.d_seq + s * self.L * 64, self.L, N_HEAD,
-                                                N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH)
-        assert ok
+        """One decode step of all layers: a captured graph (the fused append +
+        split-KV kernel and the merge), one graph launch per step."""
+        if self.bgraphs is None:
+            self.bgraphs = []
+            for r in range(self.R):
+                assert self.lib.q4_hip_graph_begin() == 1
+                ok = self._enqueue_batched(r)
+                g = self.lib.q4_hip_graph_end()
+                assert ok and g, "graph capture failed"
+                self.bgraphs.append(g)
+        assert self.lib.q4_hip_graph_launch(self.bgraphs[s])
+
+    def kernel_time(self, rounds=8):
+        """Average duration of the fused step kernel from HIP events the
+        library records around it on its stream. Each round queues a 2 GiB
+        device copy first and all selection sets' steps behind it, so the
+        steps run back to back once the copy ends and host enqueue gaps do not
+        enter the event intervals."""
+        lib, rt = self.lib, self.rt
+        n = 2 << 30
+        if self.pad is None:
+            self.pad = (rt.alloc(n), rt.alloc(n))
+        tot_ms, n_tot = 0.0, 0
+        for i in range(rounds + 1):
+            assert lib.q4_hip_copy(self.pad[1], self.pad[0], n // 4)
+            assert lib.q4kv_prof_begin(self.R)
+            assert all(self._enqueue_batched(r) for r in range(self.R))
+            t = C.c_double()
+            k = lib.q4kv_prof_end(C.byref(t))
+            assert k == self.R, f"prof_end returned {k}"
+            if i:  # the first round warms up
+                tot_ms += t.value
+                n_tot += k
+        rt.sync()
+        return tot_ms / n_tot
 
     def _enqueue_sequential(self, s):
         lib = self.lib
@@ -298,15 +338,18 @@ def main():
         return
     b = Bench(args.layers, args.sets)
     res = {}
+    kern_ms = None
     if args.mode in ("batched", "both"):
-        res["batched"] = b.timed(b.step_batched, args.steps, args.warmup, prof=True)
+        res["batched"] = b.timed(b.step_batched, args.steps, args.warmup)
+        kern_ms = b.kernel_time()
     if args.mode in ("sequential", "both"):
         res["sequential"] = b.timed(b.step_sequential, args.steps, args.warmup)
     g_us, g_gbs = b.gather_ceiling()
     threads = min(16, os.cpu_count() or 1)
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
     head = "batched" if "batched" in res else "sequential"
-    wall, gpu_s, kern_s = res[head]
+    wall, gpu_s, _ = res[head]
+    kern_s = kern_ms if head == "batched" else None
     K, L = args.steps, args.layers
     value = K * L * LAYER_B / wall / 1e9
     out = {
@@ -332,7 +375,7 @@ def main():
         ach = L * SPLIT_KERNEL_B / (kern_s / 1e3) / 1e9
         out["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_GBS,
                            "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4), "traffic": None,
-                           "kernel": "qsa_q8d256_k<MODE_BATCH>",
+                           "kernel": "qsa_q8d256_k<MODE_STEP>",
                            "kernel_us": round(kern_s * 1e3, 3),
                            "bytes_per_launch": L * SPLIT_KERNEL_B}
     out["gather_ceiling"] = {

@@ -125,6 +125,21 @@ bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n_seq,
                              uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
                              int kv_f16, uint32_t max_n);
 
+/* One decode step of one item: append the token's K and V rows at pos, then
+ * attend -- q4_hip_kv_append_batch followed by q4_hip_qsa_decode_batch, in
+ * one launch when the cache is q8_0 with head_dim 256. The attention sees
+ * the new row wherever its position list names pos. 96 bytes, device memory. */
+typedef struct {
+    q4kv_seq_desc seq;      /* caches, query, gate, output, position lists */
+    const float *k, *v;     /* the token's rows, [n_kvh][hd] fp32 each */
+    uint32_t pos;           /* cache position the rows are written at (< max_kv) */
+    uint32_t reserved[3];
+} q4kv_step_desc;
+
+bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32_t n_head,
+                           uint32_t n_kvh, uint32_t hd, float scale, int kv_f16,
+                           uint32_t max_n);
+
 /* One token's K/V rows for one cache, for a batched append. */
 typedef struct {
     void *kcache, *vcache; /* cache bases (token 0) */

@@ -43,7 +43,10 @@ typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 
-enum { MODE_DENSE = 0, MODE_INDEXED = 1, MODE_BATCH = 2 };
+/* MODE_STEP: MODE_BATCH over q4kv_step_desc entries, with the token's K/V
+ * append done by the same launch (fast q8_0 kernel only). */
+enum { MODE_DENSE = 0, MODE_INDEXED = 1, MODE_BATCH = 2, MODE_STEP = 3 };
+#define IS_BATCH(M) ((M) == MODE_BATCH || (M) == MODE_STEP)
 
 struct AttnArgs {
     const uint8_t *kc, *vc;
@@ -52,6 +55,7 @@ struct AttnArgs {
     const int32_t *idx;
     uint64_t tok_stride, kvh_stride;
     const q4kv_seq_desc *seqs;
+    uint32_t desc_stride; /* bytes between descriptors (64, or 96 for steps) */
     float *part;
     uint32_t width, kv_base, max_kv;
     uint32_t n_head, n_kvh, hd;
@@ -69,6 +73,9 @@ struct Item {
      * 0) for a dense item, so that loads and selects need no branch */
     const int32_t *lsrc;
     uint32_t lmask;
+    /* MODE_STEP: this KV head's new K/V rows and their position */
+    const float *knew, *vnew;
+    uint32_t pos_new;
 };
 
 template <int MODE>
@@ -77,8 +84,11 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
     const uint32_t gqa = a.n_head / a.n_kvh;
     const size_t hoff = (size_t)kh * gqa * a.hd;
     Item it;
-    if (MODE == MODE_BATCH) {
-        const q4kv_seq_desc *d = a.seqs + t;
+    it.knew = it.vnew = nullptr;
+    it.pos_new = ~0u;
+    if (IS_BATCH(MODE)) {
+        const q4kv_seq_desc *d =
+            (const q4kv_seq_desc *)((const uint8_t *)a.seqs + (size_t)t * a.desc_stride);
         const float *gate = ldg(&d->gate);
         const int32_t *idx = ldg(&d->idx);
         const uint32_t n_sel = ldg(&d->n_sel);
@@ -92,6 +102,12 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
         it.n = idx ? n_sel : (n_sel < it.max_kv ? n_sel : it.max_kv);
         it.lsrc = idx ? it.list : (const int32_t *)a.seqs;
         it.lmask = idx ? ~0u : 0u;
+        if (MODE == MODE_STEP) {
+            const q4kv_step_desc *sd = (const q4kv_step_desc *)d;
+            it.knew = ldg(&sd->k) + (size_t)kh * a.hd;
+            it.vnew = ldg(&sd->v) + (size_t)kh * a.hd;
+            it.pos_new = ldg(&sd->pos);
+        }
     } else {
         const size_t qo = (size_t)t * a.n_head * a.hd + hoff;
         it.kc = a.kc;
@@ -135,17 +151,6 @@ __device__ static inline float pair32_sum(float v) {
  * canonicalisations of both operands). */
 __device__ static inline float fmax2(float a, float b) {
     return __builtin_amdgcn_fmed3f(a, b, INFINITY);
-}
-
-__device__ static inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ static inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
 }
 
 /* Four signed bytes -> four exact fp16 (1024 + (b ^ 0x80) - 1152). */
@@ -259,7 +264,7 @@ __device__ static inline void pos_issue(const Item &it, const uint32_t (&j)[N],
 template <int N, int MODE>
 __device__ static inline void pos_finish(const Item &it, const uint32_t (&j)[N],
                                          const int32_t (&raw)[N], int32_t (&p)[N]) {
-    const uint32_t m = MODE == MODE_INDEXED ? ~0u : (MODE == MODE_BATCH ? it.lmask : 0u);
+    const uint32_t m = MODE == MODE_INDEXED ? ~0u : (IS_BATCH(MODE) ? it.lmask : 0u);
 #pragma unroll
     for (int u = 0; u < N; u++) {
         const int32_t r = (int32_t)(((uint32_t)raw[u] & m) | (j[u] & ~m));
@@ -749,6 +754,18 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     const uint32_t k_esel = jg == 3u ? 0x05040302u : 0x07060504u;
     const uint8_t *kbase = it.kc + (size_t)kh * ROWB, *vbase = it.vc + (size_t)kh * ROWB;
 
+    /* MODE_STEP: threads 0-63 hold four fp32 of the token's K row, 64-127 of
+     * its V row (block (tid >> 3) & 7, part tid & 7); split 0 writes the
+     * quantised rows to the caches, and any split whose chunk lists the
+     * position uses the same bytes in LDS instead of the fetched row */
+    float nx[4] = {0.f, 0.f, 0.f, 0.f};
+    const bool step_lane = MODE == MODE_STEP && tid < 128u;
+    if (step_lane) {
+        const float *src = (tid < 64u ? it.knew : it.vnew) + 32u * ((tid >> 3) & 7u) + 4u * (tid & 7u);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) nx[i] = ldg(src + i);
+    }
+
     /* rows this lane DMAs (u < 4 always valid, u = 4 only in wave 0) and the
      * s_pos entry of thread tid */
     uint32_t jcur[NLD + 1];
@@ -769,6 +786,12 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     } else {
         for (uint32_t e = tid; e < gqa * 256u; e += 256u)
             qraw[(e >> 8) * 260u + (e & 255u)] = ldg(it.q + e);
+    }
+    if (MODE == MODE_STEP && s == 0u && it.pos_new < it.max_kv && tid < 128u) {
+        int q[4];
+        const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
+        uint8_t *row = (uint8_t *)(tid < 64u ? kbase : vbase) + (size_t)it.pos_new * rstride;
+        q8_lane_store(row + 34u * ((tid >> 3) & 7u), tid & 7u, d, q);
     }
     h8_t qa[8];
     TRACE(1);
@@ -807,7 +830,22 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         }
         TRACE(2);
         __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        if (MODE == MODE_STEP) {
+            /* rows at the appended position take the new token's bytes */
+            const bool mine = tid < CP && pidx[NLD] >= 0 && (uint32_t)pidx[NLD] == it.pos_new;
+            if (__syncthreads_or(mine)) {
+                if (tid < 128u) {
+                    int q[4];
+                    const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
+                    uint8_t *base = (tid < 64u ? kraw : vraw) + 34u * ((tid >> 3) & 7u);
+                    for (uint32_t r = 0; r < CP; r++)
+                        if ((uint32_t)s_pos[r] == it.pos_new) q8_lane_store(base + r * ROWB, tid & 7u, d, q);
+                }
+                __syncthreads();
+            }
+        } else {
+            __syncthreads();
+        }
         TRACE(3);
         if (c == c0) {
             const float *qr = qraw + (g < gqa ? g : 0u) * 260u;
@@ -1130,6 +1168,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
      * resident, the generic one about as many; more splits than that only
      * add a second round of workgroups and more partials to merge. */
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
+    if (MODE == MODE_STEP && !fast) return false; /* the fused append needs the fast kernel */
     uint32_t S = (split_target() + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
@@ -1151,10 +1190,12 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
         if (fast)
             qsa_q8d256_k<MODE><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (MODE == MODE_STEP)
+            return false;
         else if (gqa <= 8u)
-            qsa_attn_k<KIND, MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
+            qsa_attn_k<KIND, MODE == MODE_STEP ? MODE_BATCH : MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
         else
-            qsa_attn_k<KIND, MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
+            qsa_attn_k<KIND, MODE == MODE_STEP ? MODE_BATCH : MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n++ + 1], q4kv_stream);
         if (S > 1u) qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
     }
@@ -1260,6 +1301,26 @@ extern "C" bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n
     AttnArgs a = base_args(nullptr, nullptr, nullptr, nullptr, nullptr, n_head, n_kvh, hd, 0,
                            scale);
     a.seqs = d_descs;
+    a.desc_stride = sizeof(q4kv_seq_desc);
+    return launch_attn<MODE_BATCH>(kv_f16, a, n_seq * n_kvh, max_n);
+}
+
+extern "C" bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq,
+                                      uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
+                                      int kv_f16, uint32_t max_n) {
+    if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
+        return false;
+    (void)hipGetLastError();
+    AttnArgs a = base_args(nullptr, nullptr, nullptr, nullptr, nullptr, n_head, n_kvh, hd, 0,
+                           scale);
+    a.seqs = (const q4kv_seq_desc *)d_descs;
+    a.desc_stride = sizeof(q4kv_step_desc);
+    const uint32_t gqa = n_head / n_kvh;
+    if (kv_f16 == Q4KV_Q8 && hd == 256u && gqa <= 8u)
+        return launch_kind<Q4KV_Q8, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa);
+    /* other widths and shapes: the append launch, then the attention */
+    const uint32_t row = kv_f16 == Q4KV_Q8 ? hd / 32u * 34u : hd * (kv_f16 == Q4KV_F16 ? 2u : 4u);
+    if (!q4kv_append_steps(d_descs, n_seq, n_kvh * hd, n_kvh * row, kv_f16)) return false;
     return launch_attn<MODE_BATCH>(kv_f16, a, n_seq * n_kvh, max_n);
 }
 

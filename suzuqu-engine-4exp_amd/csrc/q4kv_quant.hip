@@ -45,26 +45,9 @@ __device__ static void q8_quant_wg(const float *__restrict__ src, uint8_t *__res
             x0 = ldg(p); x1 = ldg(p + 1); x2 = ldg(p + 2); x3 = ldg(p + 3);
         }
     }
-    float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
-    a = fmaxf(a, __shfl_xor(a, 1, 8));
-    a = fmaxf(a, __shfl_xor(a, 2, 8));
-    a = fmaxf(a, __shfl_xor(a, 4, 8));
-    const float d = __fdiv_rn(a, 127.f);
-    const float id = d > 0.f ? __fdiv_rn(1.f, d) : 0.f;
     int q[4];
-    const float xs[4] = {x0, x1, x2, x3};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int v = (int)__builtin_rintf(__fmul_rn(xs[i], id));
-        v = v > 127 ? 127 : v;
-        v = v < -127 ? -127 : v;
-        q[i] = v;
-    }
-    uint8_t *o = ob + lb * 34u;
-    /* The block's int8 payload starts 2 bytes in, so 16-bit LDS stores. */
-    *(uint16_t *)(o + 2u + part * 4u) = (uint16_t)((q[0] & 0xff) | ((q[1] & 0xff) << 8));
-    *(uint16_t *)(o + 4u + part * 4u) = (uint16_t)((q[2] & 0xff) | ((q[3] & 0xff) << 8));
-    if (part == 0) *(uint16_t *)o = __half_as_ushort(__float2half_rn(d));
+    const float d = q8_lane_quant(x0, x1, x2, x3, q);
+    q8_lane_store(ob + lb * 34u, part, d, q);
     __syncthreads();
     const uint64_t nb = nblocks - blk0 < QBLK_PER_WG ? nblocks - blk0 : QBLK_PER_WG;
     uint8_t *out = dst + blk0 * 34u;
@@ -131,13 +114,33 @@ __global__ __launch_bounds__(256) static void kv_append_k(const float *__restric
 
 /* One launch appending a token's rows into several caches (layers or
  * sequences): grid.z selects the descriptor. Each descriptor carries its own
- * caches, fp32 rows and token position, so no device position is needed. */
-__global__ __launch_bounds__(256) static void kv_append_batch_k(const q4kv_append_desc *__restrict__ ds,
+ * caches, fp32 rows and token position, so no device position is needed.
+ * STEP: the descriptors are q4kv_step_desc (the append half of a decode
+ * step), otherwise q4kv_append_desc. */
+template <bool STEP>
+__global__ __launch_bounds__(256) static void kv_append_batch_k(const void *__restrict__ dsv,
                                                                 uint32_t n, uint32_t bpt, int kind) {
-    const q4kv_append_desc *d = ds + blockIdx.z;
-    const size_t off = (size_t)ldg(&d->pos) * bpt;
-    const float *src = blockIdx.y ? ldg(&d->v) : ldg(&d->k);
-    uint8_t *dst = (uint8_t *)(blockIdx.y ? ldg(&d->vcache) : ldg(&d->kcache)) + off;
+    const float *kf, *vf;
+    uint8_t *kc, *vc;
+    uint32_t pos;
+    if (STEP) {
+        const q4kv_step_desc *d = (const q4kv_step_desc *)dsv + blockIdx.z;
+        kf = ldg(&d->k);
+        vf = ldg(&d->v);
+        kc = (uint8_t *)ldg(&d->seq.kcache);
+        vc = (uint8_t *)ldg(&d->seq.vcache);
+        pos = ldg(&d->pos);
+    } else {
+        const q4kv_append_desc *d = (const q4kv_append_desc *)dsv + blockIdx.z;
+        kf = ldg(&d->k);
+        vf = ldg(&d->v);
+        kc = (uint8_t *)ldg(&d->kcache);
+        vc = (uint8_t *)ldg(&d->vcache);
+        pos = ldg(&d->pos);
+    }
+    const size_t off = (size_t)pos * bpt;
+    const float *src = blockIdx.y ? vf : kf;
+    uint8_t *dst = (blockIdx.y ? vc : kc) + off;
     if (kind == Q4KV_Q8) {
         const bool s_al = ((uintptr_t)src & 15u) == 0;
         const bool d_al = ((uintptr_t)dst & 15u) == 0;
@@ -153,16 +156,29 @@ __global__ __launch_bounds__(256) static void kv_append_batch_k(const q4kv_appen
     }
 }
 
-extern "C" bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc,
-                                       uint32_t n, uint32_t bpt, int kind) {
+static bool append_batch(const void *d_descs, bool step, uint32_t n_desc, uint32_t n,
+                         uint32_t bpt, int kind) {
     if (!q4kv_ok || !d_descs || !n_desc || !n || !bpt || n_desc > 65535u) return false;
     if (kind < Q4KV_F32 || kind > Q4KV_Q8) return false;
     if (kind == Q4KV_Q8 && (n % 32u)) return false;
     (void)hipGetLastError();
     const uint32_t gx = kind == Q4KV_Q8 ? (n / 32u + QBLK_PER_WG - 1) / QBLK_PER_WG
                                         : (n + 255u) / 256u;
-    kv_append_batch_k<<<dim3(gx, 2, n_desc), 256, 0, q4kv_stream>>>(d_descs, n, bpt, kind);
+    if (step)
+        kv_append_batch_k<true><<<dim3(gx, 2, n_desc), 256, 0, q4kv_stream>>>(d_descs, n, bpt, kind);
+    else
+        kv_append_batch_k<false><<<dim3(gx, 2, n_desc), 256, 0, q4kv_stream>>>(d_descs, n, bpt, kind);
     return q4kv_launch_ok("kv_append_batch");
+}
+
+bool q4kv_append_steps(const void *d_step_descs, uint32_t n_desc, uint32_t n, uint32_t bpt,
+                       int kind) {
+    return append_batch(d_step_descs, true, n_desc, n, bpt, kind);
+}
+
+extern "C" bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc,
+                                       uint32_t n, uint32_t bpt, int kind) {
+    return append_batch(d_descs, false, n_desc, n, bpt, kind);
 }
 
 extern "C" bool q4_hip_f32_to_q8(void *dst_q8, const float *src, uint64_t n) {

@@ -36,6 +36,17 @@ class SeqDesc(C.Structure):
 assert C.sizeof(SeqDesc) == 64
 
 
+class StepDesc(C.Structure):
+    """q4kv_step_desc of include/q4kv.h (96 bytes): a SeqDesc plus the
+    token's K/V rows and their cache position."""
+
+    _fields_ = [("seq", SeqDesc), ("k", _vp), ("v", _vp), ("pos", _u32),
+                ("reserved", _u32 * 3)]
+
+
+assert C.sizeof(StepDesc) == 96
+
+
 class AppendDesc(C.Structure):
     """q4kv_append_desc of include/q4kv.h (40 bytes)."""
 
@@ -89,6 +100,7 @@ SIGNATURES = {
     "q4_hip_qsa_decode_idx_kv": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u64, _u64, _u32,
                                       _u32, _u32, _u32, _u32, _f32, C.c_int]),
     "q4_hip_qsa_decode_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32]),
+    "q4_hip_qsa_step_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32]),
     "q4_hip_host_alloc": (_vp, [C.c_size_t]),
     "q4_hip_host_free": (None, [_vp]),
     "q4kv_timer_begin": (_b, [C.c_int]),

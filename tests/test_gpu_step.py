@@ -1,0 +1,156 @@
+"""q4_hip_qsa_step_batch -- a decode step's K/V append and attention in one
+launch -- against the two launches it stands for (q4_hip_kv_append_batch,
+then q4_hip_qsa_decode_batch) on the same inputs: cache bytes and outputs
+bit-identical, and the outputs against the oracle over the appended cache."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import q4kv
+from gpu_util import note
+from synth import WIDTH, assert_attn_close, heads, selection
+
+pytestmark = pytest.mark.gpu
+
+N_HEAD, N_KVH, HD = 16, 2, 256
+
+
+def _case(rng, oracle, n_seq, ctx, kind, pos_of, sel_of):
+    """Host data of n_seq items: caches holding positions < pos, the new
+    token's rows, queries and per-KV-head lists."""
+    bpt = q4kv.token_bytes(kind, N_KVH, HD)
+    items = []
+    for s in range(n_seq):
+        pos = pos_of(s)
+        k, v = heads(rng, (ctx, N_KVH)), heads(rng, (ctx, N_KVH))
+        k[pos:] = 0.0
+        v[pos:] = 0.0
+        kn, vn = heads(rng, (N_KVH,)), heads(rng, (N_KVH,))
+        q = heads(rng, (1, N_HEAD))
+        sel = sel_of(rng, s, pos)
+        enc = (lambda x: oracle.encode(x, kind))
+        items.append(dict(pos=pos, kc=enc(k), vc=enc(v), kn=kn, vn=vn, q=q, sel=sel,
+                          k=k, v=v))
+    return items, bpt
+
+
+def _run(rt, items, ctx, kind, fused, dense=False):
+    """Run one step for every item; returns (caches, outputs) downloaded."""
+    n_seq = len(items)
+    ptrs = []
+    before = set(rt._owned)
+    steps = (q4kv.StepDesc * n_seq)()
+    seqs = (q4kv.SeqDesc * n_seq)()
+    apps = (q4kv.AppendDesc * n_seq)()
+    for s, it in enumerate(items):
+        kc, vc = rt.upload(it["kc"]), rt.upload(it["vc"])
+        dkn, dvn, dq = rt.upload(it["kn"]), rt.upload(it["vn"]), rt.upload(it["q"])
+        do = rt.alloc(it["q"].nbytes)
+        rt.h2d(do, np.full(it["q"].size, np.nan, np.float32))
+        di = None if dense else rt.upload(it["sel"])
+        n_sel = it["pos"] + 1 if dense else it["sel"].shape[-1]
+        stride = 0 if dense else it["sel"].shape[-1]
+        seqs[s] = q4kv.SeqDesc(kc, vc, dq, None, do, di, n_sel, stride, ctx, 0)
+        steps[s] = q4kv.StepDesc(seqs[s], dkn, dvn, it["pos"])
+        apps[s] = q4kv.AppendDesc(kc, vc, dkn, dvn, it["pos"], 0)
+        ptrs.append((kc, vc, do))
+    max_n = max((it["pos"] + 1) if dense else it["sel"].shape[-1] for it in items)
+    lib = rt.lib
+    if fused:
+        dd = rt.alloc(ctypes.sizeof(steps))
+        assert lib.q4_hip_h2d(dd, ctypes.addressof(steps), ctypes.sizeof(steps))
+        assert lib.q4_hip_qsa_step_batch(dd, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, kind, max_n)
+    else:
+        da = rt.alloc(ctypes.sizeof(apps))
+        ds = rt.alloc(ctypes.sizeof(seqs))
+        assert lib.q4_hip_h2d(da, ctypes.addressof(apps), ctypes.sizeof(apps))
+        assert lib.q4_hip_h2d(ds, ctypes.addressof(seqs), ctypes.sizeof(seqs))
+        bpt = q4kv.token_bytes(kind, N_KVH, HD)
+        assert lib.q4_hip_kv_append_batch(da, n_seq, N_KVH * HD, bpt, kind)
+        assert lib.q4_hip_qsa_decode_batch(ds, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, kind, max_n)
+    rt.sync()
+    caches, outs = [], []
+    for (kc, vc, do), it in zip(ptrs, items):
+        caches.append((rt.download(kc, it["kc"].nbytes, np.uint8),
+                       rt.download(vc, it["vc"].nbytes, np.uint8)))
+        outs.append(rt.download(do, it["q"].nbytes, np.float32).reshape(it["q"].shape))
+    for p in [p for p in rt._owned if p not in before]:
+        rt.free(p)
+    return caches, outs
+
+
+def _check(rt, oracle, items, ctx, kind, dense=False, what=""):
+    note(f"step batch {what}")
+    c1, o1 = _run(rt, items, ctx, kind, fused=True, dense=dense)
+    c2, o2 = _run(rt, items, ctx, kind, fused=False, dense=dense)
+    for s, it in enumerate(items):
+        assert np.array_equal(c1[s][0], c2[s][0]) and np.array_equal(c1[s][1], c2[s][1]), \
+            f"{what}: cache bytes differ, item {s}"
+        assert np.array_equal(o1[s], o2[s]), f"{what}: outputs differ, item {s}"
+        # the appended row is the encoding of the new token
+        bpt = q4kv.token_bytes(kind, N_KVH, HD)
+        p = it["pos"]
+        assert np.array_equal(c1[s][0][p * bpt:(p + 1) * bpt], oracle.encode(it["kn"], kind))
+        k = it["k"].copy()
+        v = it["v"].copy()
+        k[p], v[p] = it["kn"], it["vn"]
+        kq, vq = oracle.encode(k, kind), oracle.encode(v, kind)
+        if dense:
+            want = oracle.attn(it["q"], kq, vq, kind, N_HEAD, N_KVH, HD, 1, kv_base=p,
+                               max_kv=ctx, scale=1.0 / 16)
+        else:
+            w = it["sel"].shape[-1]
+            want = oracle.attn(it["q"], kq, vq, kind, N_HEAD, N_KVH, HD, 1, idx=it["sel"],
+                               width=w, tok_stride=N_KVH * w, kvh_stride=w, max_kv=ctx,
+                               scale=1.0 / 16)
+        assert_attn_close(o1[s], want, what=f"{what} item {s}")
+
+
+def _sel_kv(rng, s, pos):
+    return np.stack([selection(rng, pos) for _ in range(N_KVH)])
+
+
+def test_step_batch_q8_matches_append_then_decode(rt, oracle):
+    """12 layers, new position inside each list (the list's last entry)."""
+    rng = np.random.default_rng(900)
+    ctx = 16384
+    items, _ = _case(rng, oracle, 12, ctx, q4kv.KV_Q8, lambda s: ctx - 1 - 600 * s, _sel_kv)
+    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what="q8 12 layers")
+
+
+def test_step_batch_position_anywhere_in_list(rt, oracle):
+    """The new position listed first, in a middle chunk and twice, or not at
+    all (then only the cache write shows it)."""
+    rng = np.random.default_rng(901)
+    ctx = 8192
+
+    def sel_of(rng, s, pos):
+        base = np.stack([selection(rng, pos - 1) for _ in range(N_KVH)])
+        if s == 0:
+            base[:, 0] = pos                      # first chunk
+        elif s == 1:
+            base[:, 1000] = pos                   # a middle chunk (another split)
+        elif s == 2:
+            base[:, 70] = pos                     # twice, two chunks
+            base[:, 2000] = pos
+        return base                               # s == 3: not listed
+    items, _ = _case(rng, oracle, 4, ctx, q4kv.KV_Q8, lambda s: 5000 + 37 * s, sel_of)
+    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what="position anywhere")
+
+
+def test_step_batch_dense_items(rt, oracle):
+    """Dense items (no list): positions 0 .. pos, the new one last."""
+    rng = np.random.default_rng(902)
+    ctx = 4096
+    items, _ = _case(rng, oracle, 3, ctx, q4kv.KV_Q8, lambda s: 1000 + 1500 * s, _sel_kv)
+    _check(rt, oracle, items, ctx, q4kv.KV_Q8, dense=True, what="dense")
+
+
+@pytest.mark.parametrize("kind", [q4kv.KV_F16, q4kv.KV_F32])
+def test_step_batch_other_widths(rt, oracle, kind):
+    """f16 / f32 caches take the append launch then the attention launch."""
+    rng = np.random.default_rng(903 + kind)
+    ctx = 4096
+    items, _ = _case(rng, oracle, 3, ctx, kind, lambda s: ctx - 1 - 300 * s, _sel_kv)
+    _check(rt, oracle, items, ctx, kind, what=f"width {kind}")
