@@ -1121,7 +1121,11 @@ extern "C" bool q4kv_prof_begin(int max_launches) {
     if (!q4kv_ok || q4kv_capturing || max_launches <= 0 || max_launches > Q4KV_PROF_MAX)
         return false;
     for (; g_pev_made < 2 * max_launches; g_pev_made++)
-        if (hipEventCreate(&g_pev[g_pev_made]) != hipSuccess) return false;
+        /* timing-only events: no system-scope fence (cache writeback and
+         * invalidate) when they complete, which would add to the interval */
+        if (hipEventCreateWithFlags(&g_pev[g_pev_made], hipEventDisableSystemFence) !=
+            hipSuccess)
+            return false;
     g_prof_on = 1;
     g_prof_n = 0;
     g_prof_max = max_launches;
