@@ -23,7 +23,9 @@
  *    folded into the weights before the fp16 split (PV).
  *  - int8 -> fp16 is exact and branch-free: v_perm_b32 places each byte
  *    (xor 0x80) under the exponent 0x64 (1024 + u), one packed subtract of
- *    1152 leaves the signed value.
+ *    1152 leaves the signed value. The q8_0 fast kernel skips the subtract and
+ *    removes the bias on the MFMA pipe instead (accumulator input q x -1152
+ *    for Q.K, one more MFMA with a -1152 operand for P.V).
  *  - Online softmax in base 2 per chunk; the split partials (m, l, acc[hd])
  *    are merged by a second kernel that also applies the gate. A single
  *    split (prefill, or short lists) finalises in place.
@@ -794,6 +796,10 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         q8_lane_store(row + 34u * ((tid >> 3) & 7u), tid & 7u, d, q);
     }
     h8_t qa[8];
+    /* K operands stay biased by +1152 (the exponent trick's 1024 + 128);
+     * qbias[b] = qa[b] x (-1152) is the MFMA accumulator input that removes
+     * the bias, computed once per workgroup */
+    f4_t qbias[8];
     TRACE(1);
     float m_run[4], l_run[4];
     f4_t acc[4];
@@ -858,6 +864,11 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                     qa[b][2u * kk] = split_sel(v[0] * qs, nsel);
                     qa[b][2u * kk + 1u] = split_sel(v[1] * qs, nsel);
                 }
+            const h8_t neg = (h8_t)((_Float16)-1152.0f);
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++)
+                qbias[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[b], neg,
+                                                                  (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         }
         if (c + 1u < c1) {
 #pragma unroll
@@ -892,10 +903,9 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             uint32_t r0, r1, r2, r3;
             i8x4_to_h4(w0, r0, r1);
             i8x4_to_h4(w1, r2, r3);
-            const h8_t kb = h8_minus_1152((u4_t){r0, r1, r2, r3});
+            const h8_t kb = __builtin_bit_cast(h8_t, (u4_t){r0, r1, r2, r3}); /* 1152 + k */
             const float ks = ld_f16(krow + 34u * b);
-            const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                qa[b], kb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[b], kb, qbias[b], 0, 0, 0);
             S += ks * C;
         }
         TRACE(4);
@@ -961,10 +971,16 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 h8_t A;
 #pragma unroll
                 for (uint32_t i = 0; i < 8u; i++) A[i] = split_sel(wp[i] * sp[i], nsel);
-                acc[2u * u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, h8_minus_1152(r0),
-                                                                    acc[2u * u], 0, 0, 0);
+                /* biased V (1152 + v): the bias leaves with A x (-1152), on the
+                 * otherwise idle MFMA pipe */
+                const h8_t neg = (h8_t)((_Float16)-1152.0f);
+                acc[2u * u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, neg, acc[2u * u], 0, 0, 0);
+                acc[2u * u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    A, __builtin_bit_cast(h8_t, r0), acc[2u * u], 0, 0, 0);
+                acc[2u * u + 1u] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(A, neg, acc[2u * u + 1u], 0, 0, 0);
                 acc[2u * u + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    A, h8_minus_1152(r1), acc[2u * u + 1u], 0, 0, 0);
+                    A, __builtin_bit_cast(h8_t, r1), acc[2u * u + 1u], 0, 0, 0);
             }
         }
         TRACE(9);
