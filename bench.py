@@ -301,6 +301,224 @@ class Bench:
         return res, cpu
 
 
+# ---------------------------------------------------------------------------
+# The other BASELINE configurations, measured beside the headline (extra keys
+# under "configs"; the headline `value` stays config 1).
+
+
+def _graphs(lib, enqueue, n):
+    """One captured graph per set (the reference's decode-graph pattern)."""
+    out = []
+    for r in range(n):
+        assert lib.q4_hip_graph_begin() == 1
+        ok = enqueue(r)
+        g = lib.q4_hip_graph_end()
+        assert ok and g, "graph capture failed"
+        out.append(g)
+    return out
+
+
+def _time_graphs(b, graphs, steps):
+    lib = b.lib
+    for i in range(8):
+        assert lib.q4_hip_graph_launch(graphs[i % len(graphs)])
+    b.rt.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        assert lib.q4_hip_graph_launch(graphs[i % len(graphs)])
+    b.rt.sync()
+    wall = time.perf_counter() - t0
+    for g in graphs:
+        lib.q4_hip_graph_free(g)
+    return wall / steps
+
+
+def _fill(b, ptr, n_tok, kind, seed):
+    """Synthetic K or V rows for n_tok tokens written at ptr in width kind."""
+    rt, lib = b.rt, b.lib
+    n = n_tok * N_KVH * HD
+    tmp = rt.alloc(n * 4)
+    b.gen(tmp, n, seed)
+    if kind == q4kv.KV_Q8:
+        assert lib.q4_hip_f32_to_q8(ptr, tmp, n)
+    elif kind == q4kv.KV_F16:
+        assert lib.q4_hip_f32_to_f16(ptr, tmp, n)
+    else:
+        assert lib.q4_hip_copy(ptr, tmp, n)
+    rt.sync()
+    rt.free(tmp)
+
+
+def config2(b, steps=200, sets=4):
+    """Config 2: 32 sequences, contexts log-uniform in [8192, 131072], own
+    q8_0 caches; one step = every sequence's append + sparse attention
+    (q4_hip_qsa_step_batch)."""
+    rt, lib = b.rt, b.lib
+    rng = np.random.default_rng(1236)
+    n_seq = 32
+    lens = np.exp(rng.uniform(np.log(8192), np.log(131072), n_seq)).astype(np.int64)
+    ptrs = []
+    caches = []
+    for s_ in range(n_seq):
+        L = int(lens[s_])
+        kc, vc = rt.alloc(L * BPT), rt.alloc(L * BPT)
+        _fill(b, kc, L, q4kv.KV_Q8, 3000 + 2 * s_)
+        _fill(b, vc, L, q4kv.KV_Q8, 3001 + 2 * s_)
+        caches.append((kc, vc, L))
+    dq = rt.alloc(sets * n_seq * QO_B)
+    dnk = rt.alloc(sets * n_seq * N_KVH * HD * 4)
+    dnv = rt.alloc(sets * n_seq * N_KVH * HD * 4)
+    b.gen(dq, sets * n_seq * N_HEAD * HD, 3500)
+    b.gen(dnk, sets * n_seq * N_KVH * HD, 3501)
+    b.gen(dnv, sets * n_seq * N_KVH * HD, 3502)
+    dout = rt.alloc(n_seq * QO_B)
+    sel = np.empty((sets, n_seq, N_KVH, WIDTH), np.int32)
+    for r in range(sets):
+        for s_, (_, _, L) in enumerate(caches):
+            for h in range(N_KVH):
+                sel[r, s_, h] = selection(rng, L - 1 - 7 * r)
+    dsel = rt.upload(sel)
+    steps_d = (q4kv.StepDesc * (sets * n_seq))()
+    for r in range(sets):
+        for s_, (kc, vc, L) in enumerate(caches):
+            i = r * n_seq + s_
+            seq = q4kv.SeqDesc(kc, vc, dq + i * QO_B, None, dout + s_ * QO_B,
+                               dsel + i * IDX_B, WIDTH, WIDTH, L, 0)
+            row = i * N_KVH * HD * 4
+            steps_d[i] = q4kv.StepDesc(seq, dnk + row, dnv + row, L - 1 - 7 * r)
+    dd = rt.alloc(C.sizeof(steps_d))
+    assert lib.q4_hip_h2d(dd, C.addressof(steps_d), C.sizeof(steps_d))
+    sz = C.sizeof(q4kv.StepDesc)
+    graphs = _graphs(lib, lambda r: lib.q4_hip_qsa_step_batch(
+        dd + r * n_seq * sz, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH), sets)
+    t = _time_graphs(b, graphs, steps)
+    byts = n_seq * LAYER_B
+    for kc, vc, _ in caches:
+        rt.free(kc)
+        rt.free(vc)
+    for p_ in (dq, dnk, dnv, dout, dsel, dd):
+        rt.free(p_)
+    return {"what": "32 sequences (ctx log-uniform 8192-131072, seed 1236), one batched decode "
+                    "step each: q8_0 append + sparse attention over 2x2051 positions",
+            "us_per_step": round(t * 1e6, 2), "bytes_per_step": byts,
+            "gbs": round(byts / t / 1e9, 1), "pct_of_peak": round(100 * byts / t / 1e9 / PEAK_GBS, 2),
+            "steps": steps, "selection_sets": sets}
+
+
+def config3(b, reps=4):
+    """Config 3: chunked prefill -- a 16384-token q8_0 cache, an 8192-token
+    fp32 chunk quantised and appended, then every chunk token attends its own
+    list per KV head: 3 sinks + 512 recent + 1536 earlier positions."""
+    rt, lib = b.rt, b.lib
+    ctx0, chunk = 16384, 8192
+    max_kv = ctx0 + chunk
+    kc, vc = rt.alloc(max_kv * BPT), rt.alloc(max_kv * BPT)
+    _fill(b, kc, ctx0, q4kv.KV_Q8, 4000)
+    _fill(b, vc, ctx0, q4kv.KV_Q8, 4001)
+    nk, nv = rt.alloc(chunk * N_KVH * HD * 4), rt.alloc(chunk * N_KVH * HD * 4)
+    b.gen(nk, chunk * N_KVH * HD, 4002)
+    b.gen(nv, chunk * N_KVH * HD, 4003)
+    dq, dout = rt.alloc(chunk * QO_B), rt.alloc(chunk * QO_B)
+    b.gen(dq, chunk * N_HEAD * HD, 4004)
+    # lists: the 1536 earlier positions of query t per KV head are a strided
+    # pseudo-random permutation of [3, pos-511) (distinct, then sorted)
+    rng = np.random.default_rng(1237)
+    pos = ctx0 + np.arange(chunk, dtype=np.int64)
+    span = pos - 511 - 3
+    sel = np.empty((chunk, N_KVH, WIDTH), np.int32)
+    i = np.arange(1536, dtype=np.int64)
+    for h in range(N_KVH):
+        start = rng.integers(0, span)
+        step = rng.integers(1, span)
+        step = np.where(np.gcd(step, span) == 1, step, 1)
+        uni = 3 + (start[:, None] + step[:, None] * i[None, :]) % span[:, None]
+        uni.sort(axis=1)
+        sel[:, h, :3] = np.arange(3)
+        sel[:, h, 3:1539] = uni
+        sel[:, h, 1539:] = pos[:, None] - 511 + np.arange(512)[None, :]
+    dsel = rt.upload(sel)
+    off = ctx0 * BPT
+    n = chunk * N_KVH * HD
+
+    def run():
+        ok = lib.q4_hip_f32_to_q8(kc + off, nk, n) and lib.q4_hip_f32_to_q8(vc + off, nv, n)
+        return ok and lib.q4_hip_qsa_decode_idx_kv(dq, kc, vc, None, dout, dsel, WIDTH,
+                                                   N_KVH * WIDTH, WIDTH, N_HEAD, N_KVH, HD,
+                                                   chunk, max_kv, 1.0 / 16, q4kv.KV_Q8)
+    assert run()
+    rt.sync()
+    assert lib.q4kv_timer_begin(0)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        assert run()
+    rt.sync()
+    wall = (time.perf_counter() - t0) / reps
+    flop = chunk * N_HEAD * WIDTH * HD * 4
+    for p_ in (kc, vc, nk, nv, dq, dout, dsel):
+        rt.free(p_)
+    return {"what": "8192-token q8_0 chunk appended to a 16384-token cache, then 8192 "
+                    "queries x 16 heads over per-KV-head lists of 2051 (3 sinks + 512 recent "
+                    "+ 1536 earlier, strided pseudo-random)",
+            "us_per_layer": round(wall * 1e6, 1), "gflop": round(flop / 1e9, 1),
+            "tflops": round(flop / wall / 1e12, 2),
+            "pct_of_fp16_mfma_peak": round(100 * flop / wall / 2.5e15, 2), "reps": reps}
+
+
+def config4(b, steps=100, sets=4, layers=4):
+    """Config 4: config 1's decode step on f16 and f32 caches, and the
+    restore of a 100000-token x 12-layer q8_0 session image from pinned host
+    memory."""
+    rt, lib = b.rt, b.lib
+    out = {}
+    for kind, name in ((q4kv.KV_F16, "f16"), (q4kv.KV_F32, "f32")):
+        bpt = q4kv.token_bytes(kind, N_KVH, HD)
+        kcs = [rt.alloc(CTX * bpt) for _ in range(layers)]
+        vcs = [rt.alloc(CTX * bpt) for _ in range(layers)]
+        for li in range(layers):
+            _fill(b, kcs[li], CTX, kind, 5000 + 2 * li)
+            _fill(b, vcs[li], CTX, kind, 5001 + 2 * li)
+        steps_d = (q4kv.StepDesc * (sets * layers))()
+        for r in range(sets):
+            for li in range(layers):
+                i = r * layers + li
+                seq = q4kv.SeqDesc(kcs[li], vcs[li], b.q_ptr(r, li), None,
+                                   b.d_out + li * QO_B, b.sel_ptr(r, li), WIDTH, WIDTH, CTX, 0)
+                steps_d[i] = q4kv.StepDesc(seq, b.row_ptr(b.d_nk, r, li),
+                                           b.row_ptr(b.d_nv, r, li), b.pos[r])
+        dd = rt.alloc(C.sizeof(steps_d))
+        assert lib.q4_hip_h2d(dd, C.addressof(steps_d), C.sizeof(steps_d))
+        sz = C.sizeof(q4kv.StepDesc)
+        graphs = _graphs(lib, lambda r: lib.q4_hip_qsa_step_batch(
+            dd + r * layers * sz, layers, N_HEAD, N_KVH, HD, 1.0 / 16, kind, WIDTH), sets)
+        t = _time_graphs(b, graphs, steps) / layers
+        byts = 2 * N_KVH * WIDTH * (bpt // N_KVH) + IDX_B + 2 * QO_B + 2 * N_KVH * HD * 4 + 2 * bpt
+        out[name] = {"us_per_layer": round(t * 1e6, 3), "bytes_per_layer": byts,
+                     "gbs": round(byts / t / 1e9, 1), "layers_per_step": layers}
+        for p_ in kcs + vcs + [dd]:
+            rt.free(p_)
+    # session restore: 12 layers x 100000 tokens of q8_0 K and V from pinned memory
+    c = q4kv.KvCache()
+    n_img = 100000
+    assert lib.q4kv_cache_open(C.byref(c), q4kv.KV_Q8, 12, N_KVH, HD, n_img)
+    nb = lib.q4kv_image_bytes(C.byref(c), n_img)
+    host = lib.q4_hip_host_alloc(nb)
+    assert host
+    C.memset(host, 0x5A, nb)
+    assert lib.q4kv_image_restore(C.byref(c), host, n_img, True)
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        assert lib.q4kv_image_restore(C.byref(c), host, n_img, True)
+    t = (time.perf_counter() - t0) / reps
+    lib.q4_hip_host_free(host)
+    lib.q4kv_cache_close(C.byref(c))
+    out["restore"] = {"what": "12 layers x 100000 tokens q8_0 K+V image, pinned host -> "
+                              "device cache layout (host link bound)",
+                      "bytes": nb, "ms": round(t * 1e3, 2), "gbs": round(nb / t / 1e9, 2)}
+    return out
+
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -320,6 +538,8 @@ def main():
     ap.add_argument("--sets", type=int, default=16)
     ap.add_argument("--mode", choices=["batched", "sequential", "both"], default="both")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--configs", type=int, default=1,
+                    help="also measure configs 2, 3 and 4 (0 to skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (PMC calibration)")
     args = ap.parse_args()
@@ -345,6 +565,10 @@ def main():
     if args.mode in ("sequential", "both"):
         res["sequential"] = b.timed(b.step_sequential, args.steps, args.warmup)
     g_us, g_gbs = b.gather_ceiling()
+    configs = None
+    if args.configs:
+        configs = {"config2_batched_decode": config2(b), "config3_chunked_prefill": config3(b),
+                   "config4_widths_restore": config4(b)}
     threads = min(16, os.cpu_count() or 1)
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
     head = "batched" if "batched" in res else "sequential"
@@ -378,6 +602,8 @@ def main():
                            "kernel": "qsa_q8d256_k<MODE_STEP>",
                            "kernel_us": round(kern_s * 1e3, 3),
                            "bytes_per_launch": L * SPLIT_KERNEL_B}
+    if configs:
+        out["configs"] = configs
     out["gather_ceiling"] = {
         "gbs": round(g_gbs, 1), "us_per_launch": round(g_us, 3),
         "what": "the same K/V rows of one batched step DMA'd to LDS with no compute "
