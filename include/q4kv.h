@@ -87,6 +87,46 @@ bool q4_hip_qsa_decode(const float *d_q, const void *d_kcache, const void *d_vca
  * its split-KV partial buffer in q4_hip_init; this only reports it. */
 bool q4_hip_qsa_topk_alloc(void);
 
+/* ---------------- QSA indexer and Q/K preparation ----------------
+ * Shapes as the reference: hd (indexer dim) must be 128, n_head <= 4,
+ * k_blk <= 512. raw is fp16 [pos][128], pool fp32 [block][128], score fp32
+ * [tok][stride], sel int32 [tok][width]. _d variants read the position from
+ * the device counter set by q4_hip_pos_push and are graph-capture safe. */
+bool q4_hip_qsa_q_prep(const float *d_qg, const float *d_wn, float *d_q, float *d_g,
+                       uint32_t n_head, uint32_t hd, uint32_t n_rot, int32_t pos,
+                       float base, float eps);                          /* src/q4.h:895-897 */
+bool q4_hip_qsa_q_prep_n(const float *d_qg, const float *d_wn, float *d_q, float *d_g,
+                         uint32_t n_head, uint32_t hd, uint32_t n_rot, int32_t pos0,
+                         float base, float eps, uint32_t n_tok);       /* src/q4.h:898-900 */
+bool q4_hip_qsa_q_prep_d(const float *qg, const float *wn, float *q, float *g,
+                         uint32_t n_head, uint32_t hd, uint32_t n_rot,
+                         float base, float eps);                        /* src/q4.h:689-691 */
+bool q4_hip_qsa_k_prep(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
+                       uint32_t n_rot, int32_t pos, float base, float eps); /* src/q4.h:901-902 */
+bool q4_hip_qsa_k_prep_n(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
+                         uint32_t n_rot, int32_t pos0, float base, float eps,
+                         uint32_t n_tok);                               /* src/q4.h:903-905 */
+bool q4_hip_qsa_k_prep_d(float *k, const float *wn, uint32_t n_kvh, uint32_t hd,
+                         uint32_t n_rot, float base, float eps);        /* src/q4.h:692-693 */
+bool q4_hip_f32_to_f16_d(void *dst_base, uint32_t stride_elems, const float *src,
+                         uint64_t n);                                   /* src/q4.h:696-697 */
+bool q4_hip_qsa_pool(const void *raw_f16, float *pool, const float *wn, uint32_t hd,
+                     uint32_t ratio, uint32_t b0, uint32_t b1, uint32_t n_rot,
+                     float rope_base, float eps);                       /* src/q4.h:917-920 */
+bool q4_hip_qsa_pool_d(const void *raw, float *pool, const float *wn, uint32_t hd,
+                       uint32_t ratio, uint32_t n_rot, float rope_base,
+                       float eps);                                      /* src/q4.h:698-700 */
+bool q4_hip_qsa_score(const float *q, const float *pool, float *score, uint32_t n_tok,
+                      uint32_t n_blocks, uint32_t stride, uint32_t n_head, uint32_t hd,
+                      uint32_t pos0, uint32_t ratio);                   /* src/q4.h:921-924 */
+bool q4_hip_qsa_score_d(const float *q, const float *pool, float *score, uint32_t stride,
+                        uint32_t n_head, uint32_t hd, uint32_t ratio);  /* src/q4.h:701-703 */
+bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok, uint32_t n_blocks,
+                     uint32_t stride, uint32_t k_blk, uint32_t ratio, uint32_t pos0,
+                     uint32_t width);                                   /* src/q4.h:925-927 */
+bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride, uint32_t k_blk,
+                       uint32_t ratio, uint32_t width);                 /* src/q4.h:705-706 */
+
 /* ---------------- extensions (no reference counterpart) ----------------
  * Additive entry points; nothing above depends on them. */
 

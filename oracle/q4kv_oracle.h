@@ -25,6 +25,17 @@
  *                      returns V exactly, equal scores give the mean of V, an
  *                      all -1 list gives 0, permutation invariance of the list,
  *                      causal dense == indexed list 0..t, gate=0 halves output.
+ *   orc_qsa_topk       an independent sort-based brute force (numpy, stable
+ *                      argsort on (key desc, index asc)) over random, tied,
+ *                      +-0, NaN and dense-prefix rows; orc_qsa_key against
+ *                      numpy float ordering.
+ *   orc_qsa_pool       closed forms: constant raw keys pool to wn * sign
+ *   orc_qsa_prep         (RMSNorm of a constant), RoPE preserves each pair's
+ *                      norm and is the identity at position 0 and for dims
+ *                      >= n_rot; a single-pair input rotates by the angle
+ *                      formed from orc_rope_freq, which is checked against
+ *                      numpy float32 arithmetic.
+ *   orc_qsa_score      numpy float64 einsum + relu + -1e30 mask.
  */
 #ifndef Q4KV_ORACLE_H
 #define Q4KV_ORACLE_H
@@ -74,6 +85,27 @@ int orc_attn(const float *q, const void *kcache, const void *vcache, int kind,
              uint32_t hd, uint32_t n_tok, const int32_t *idx, uint32_t width,
              uint64_t tok_stride, uint64_t kvh_stride, uint32_t kv_base,
              uint32_t max_kv, float scale, int dbl, int nthreads);
+
+/* ---- QSA indexer and Q/K preparation (oracle/qsa_index_oracle.c) ---- */
+/* Order-preserving key of an fp32 score, src/q4_rocm.cu:7471-7474. */
+uint32_t orc_qsa_key(float f);
+/* fp32 RoPE frequency base^-(p/np), correctly rounded. */
+float orc_rope_freq(float base, uint32_t p, uint32_t np);
+/* One head: RMSNorm * wn then RoPE of dims < n_rot at pos
+ * (src/q4_rocm.cu:6229-6289). */
+int orc_qsa_prep(const float *src, float *dst, const float *wn, uint32_t hd,
+                 uint32_t n_rot, int32_t pos, float base, float eps);
+/* Pool blocks [b0, b1) of fp16 raw keys (src/q4_rocm.cu:7366-7401). */
+int orc_qsa_pool(const uint16_t *raw, float *pool, const float *wn, uint32_t hd,
+                 uint32_t ratio, uint32_t b0, uint32_t b1, uint32_t n_rot,
+                 float base, float eps);
+/* Block scores per token (src/q4_rocm.cu:7412-7445). */
+int orc_qsa_score(const float *q, const float *pool, float *score, uint32_t n_tok,
+                  uint32_t n_blocks, uint32_t stride, uint32_t n_head, uint32_t hd,
+                  uint32_t pos0, uint32_t ratio);
+/* Exact top-k block selection and expansion (src/q4_rocm.cu:7722-7846). */
+int orc_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok, uint32_t stride,
+                 uint32_t k_blk, uint32_t ratio, uint32_t pos0, uint32_t width);
 
 #ifdef __cplusplus
 }

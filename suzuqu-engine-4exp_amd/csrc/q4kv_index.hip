@@ -1,0 +1,743 @@
+/*
+ * q4kv_index.hip -- the QSA indexer on gfx950: pooled block keys, block
+ * scores, exact top-k block selection with expansion to a position list, and
+ * the RMSNorm + partial-RoPE preparation of queries and keys.
+ *
+ * Reference interface: src/q4.h:689-707, 895-927; kernels
+ * src/q4_rocm.cu:6229-6343 (prep) and 7366-7960 (indexer).
+ *
+ * Layouts (as the reference's callers, src/q4_fwd.c:676-770, 895-925):
+ *   raw   fp16 [pos][hd]          indexer keys, hd = 128
+ *   pool  fp32 [block][hd]        block b pools positions b*ratio .. +ratio-1
+ *   q     fp32 [tok][head][hd]    indexer queries, head < 4
+ *   score fp32 [tok][stride]      stride = max_blocks
+ *   sel   int32 [tok][width]      the attention's position list
+ *
+ * Design:
+ *   pool   one wave per block; lane l owns the RoPE pair (2l, 2l+1), so the
+ *          rotation never leaves the lane. The RoPE frequency is computed
+ *          once per lane, correctly rounded (pow in double, one rounding).
+ *   score  decode: a memory-bound stream over the pool (512 B per block);
+ *          eight lanes per block row, each lane holding 16 dims of all four
+ *          queries in registers, a 3-step DPP reduction per head.
+ *          prefill (>= 4 tokens): fp32 MFMA 16x16x4 with A rows (token, head)
+ *          so each lane's four accumulators are one token's four heads and
+ *          the relu-sum over heads stays in the lane.
+ *   topk   one 1024-thread workgroup per token row: keys live in VGPRs (64 per
+ *          thread, 65536 per chunk), four 8-bit radix passes into a 32-way
+ *          replicated LDS histogram (no same-address atomics within a
+ *          half-wave), then an ordered compaction by wave ballots + one block
+ *          scan, then the expansion. Two launches replace the reference's
+ *          eleven on the device-position path.
+ */
+#include "q4kv_internal.h"
+#include "q4kv.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr uint32_t IDX_HD = 128;
+
+/* Vector loads/stores (HIP's vector classes do not take an address-space
+ * qualified copy; these pointers are global kernel arguments). */
+template <class T> __device__ inline T ld_vec(const T *p) { return *p; }
+template <class T> __device__ inline void st_vec(T *p, T v) { *p = v; }
+
+template <int CTRL> __device__ inline float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+/* Sum over the 8-lane group containing this lane, broadcast to all 8. */
+__device__ inline float sum8(float v) {
+    v += dpp<0xB1>(v);  /* quad_perm [1,0,3,2] */
+    v += dpp<0x4E>(v);  /* quad_perm [2,3,0,1] */
+    v += dpp<0x141>(v); /* row_half_mirror: lane i <-> 7-i */
+    return v;
+}
+__device__ inline float wave_sum(float v) {
+    v = sum8(v);
+    v += dpp<0x140>(v); /* row_mirror: the other half of the 16-lane row */
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+/* fp32 RoPE frequency base^(-(p/np)) with the exponent an fp32 quotient
+ * (src/q4_rocm.cu:6255, 7391), correctly rounded: pow in double, rounded once.
+ * At positions near 2^18 one ulp of freq moves the angle by ~0.016 rad, so the
+ * frequency is not left to an approximate powf. */
+__device__ inline float rope_freq(float base, uint32_t p, uint32_t np) {
+    const float e = -__fdiv_rn((float)p, (float)np);
+    return (float)pow((double)base, (double)e);
+}
+/* Rotate (x0, x1) by the fp32 angle pos * freq (one fp32 rounding, as the
+ * reference forms it). */
+__device__ inline void rope_rotate(float &x0, float &x1, float pos_f, float freq) {
+    const float ang = __fmul_rn(pos_f, freq);
+    float s, c;
+    sincosf(ang, &s, &c);
+    const float a = x0, b = x1;
+    x0 = a * c - b * s;
+    x1 = a * s + b * c;
+}
+
+/* --------------------------------------------------------------- pool ---- */
+
+/* Pool block b into pool[b][0..128): mean of `ratio` fp16 rows, RMSNorm * wn,
+ * RoPE at position b*ratio. One wave; lane l owns dims 2l, 2l+1.
+ * src/q4_rocm.cu:7366-7401. */
+__device__ inline void pool_block(const uint32_t *raw2, float *pool, const float *wn,
+                                  uint32_t ratio, uint32_t b, uint32_t n_rot, float freq,
+                                  float eps, uint32_t lane) {
+    const uint32_t *src = raw2 + (size_t)b * ratio * (IDX_HD / 2) + lane;
+    float s0 = 0.f, s1 = 0.f;
+    uint32_t j = 0;
+    for (; j + 4 <= ratio; j += 4) {
+        uint32_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) h[i] = ldg(src + (size_t)(j + i) * (IDX_HD / 2));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s0 += __half2float(__ushort_as_half((unsigned short)(h[i] & 0xffffu)));
+            s1 += __half2float(__ushort_as_half((unsigned short)(h[i] >> 16)));
+        }
+    }
+    for (; j < ratio; j++) {
+        const uint32_t h = ldg(src + (size_t)j * (IDX_HD / 2));
+        s0 += __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
+        s1 += __half2float(__ushort_as_half((unsigned short)(h >> 16)));
+    }
+    float v0 = __fdiv_rn(s0, (float)ratio), v1 = __fdiv_rn(s1, (float)ratio);
+    const float ss = wave_sum(v0 * v0 + v1 * v1);
+    const float inv = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)IDX_HD) + eps));
+    const float w0 = wn ? ldg(wn + 2 * lane) : 1.f, w1 = wn ? ldg(wn + 2 * lane + 1) : 1.f;
+    v0 = v0 * inv * w0;
+    v1 = v1 * inv * w1;
+    if (2 * lane < n_rot) rope_rotate(v0, v1, (float)(b * ratio), freq);
+    st_vec((float2 *)(pool + (size_t)b * IDX_HD) + lane, make_float2(v0, v1));
+}
+
+__global__ __launch_bounds__(256) void qsa_pool_k(const uint32_t *raw2, float *pool,
+                                                  const float *wn, uint32_t ratio, uint32_t b0,
+                                                  uint32_t b1, uint32_t n_rot, float base,
+                                                  float eps) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const float freq = 2 * lane < n_rot ? rope_freq(base, lane, n_rot / 2) : 0.f;
+    const uint32_t nw = gridDim.x * 4u;
+    for (uint32_t b = b0 + blockIdx.x * 4u + (threadIdx.x >> 6); b < b1; b += nw)
+        pool_block(raw2, pool, wn, ratio, b, n_rot, freq, eps, lane);
+}
+
+/* Device-position variant: pools the block that position *pp completes, if
+ * any (src/q4_rocm.cu:7893-7930). */
+__global__ __launch_bounds__(64) void qsa_pool_dk(const uint32_t *raw2, float *pool,
+                                                  const float *wn, uint32_t ratio,
+                                                  uint32_t n_rot, float base, float eps,
+                                                  const int32_t *pp) {
+    const uint32_t pos = (uint32_t)*pp;
+    const uint32_t b0 = pos / ratio, b1 = (pos + 1) / ratio;
+    if (b1 <= b0) return;
+    const uint32_t lane = threadIdx.x;
+    const float freq = 2 * lane < n_rot ? rope_freq(base, lane, n_rot / 2) : 0.f;
+    pool_block(raw2, pool, wn, ratio, b0, n_rot, freq, eps, lane);
+}
+
+/* fp16 store of the raw key at the device position's row
+ * (src/q4_rocm.cu:7932-7947). */
+__global__ __launch_bounds__(256) void f16_at_k(const float *src, __half *dst0, uint32_t stride,
+                                                uint64_t n, const int32_t *pp) {
+    __half *dst = dst0 + (size_t)(uint32_t)*pp * stride;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = __float2half_rn(ldg(src + i));
+}
+
+/* -------------------------------------------------------------- score ---- */
+
+constexpr uint32_t SC_ROWS_WG = 64; /* 4 waves x 2 x 8 rows */
+
+/* Streaming block scores for few tokens (decode: one token at the device
+ * position). Token t = blockIdx.y; rows b < n_vis get sum_h relu(q_h . pool_b),
+ * n_vis <= b < n_blocks get -1e30 (src/q4_rocm.cu:7412-7445, 7476-7503).
+ * DEV: the device position bounds the rows written to b < n_vis. */
+template <bool DEV>
+__global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float *pool,
+                                                     float *score, uint32_t n_blocks,
+                                                     uint32_t stride, uint32_t n_head,
+                                                     uint32_t pos0, uint32_t ratio,
+                                                     const int32_t *pp) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t pos = (DEV ? (uint32_t)*pp : pos0) + t;
+    const uint32_t n_vis = ratio ? (pos + 1) / ratio : 0;
+    if (DEV) n_blocks = n_vis;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane & 7u, rsub = lane >> 3;
+    uint32_t rb = blockIdx.x * SC_ROWS_WG;
+    if (rb >= n_blocks) return;
+
+    /* lane g of a row group holds dims {32i + 4g .. +3 : i < 4} of each query */
+    float4 qr[4][4];
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            qr[h][i] = (uint32_t)h < n_head
+                           ? ld_vec((const float4 *)(q + ((size_t)t * n_head + h) * IDX_HD +
+                                                  32 * i + 4 * g))
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    float *srow = score + (size_t)t * stride;
+    const uint32_t rlast = n_vis ? n_vis - 1 : 0;
+    for (; rb < n_blocks; rb += gridDim.x * SC_ROWS_WG) {
+        float4 p[2][4];
+        uint32_t row[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            row[u] = rb + wave * 16u + 8u * u + rsub;
+            const uint32_t r = row[u] < rlast ? row[u] : rlast;
+            const float4 *src = (const float4 *)(pool + (size_t)r * IDX_HD) + g;
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[u][i] = ld_vec(src + 8 * i);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            float s = 0.f;
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                float d = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    d = fmaf(qr[h][i].x, p[u][i].x, d);
+                    d = fmaf(qr[h][i].y, p[u][i].y, d);
+                    d = fmaf(qr[h][i].z, p[u][i].z, d);
+                    d = fmaf(qr[h][i].w, p[u][i].w, d);
+                }
+                s += fmaxf(sum8(d), 0.f);
+            }
+            if (g == 0 && row[u] < n_blocks) srow[row[u]] = row[u] < n_vis ? s : -1.0e30f;
+        }
+    }
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+/* Block scores for a chunk of >= 4 tokens on fp32 MFMA (16x16x4). A tile =
+ * 4 tokens x 4 heads (row 4*token + head), B tile = 16 pool rows. The dot
+ * product's dims are permuted so each lane reads 32 contiguous floats of its
+ * row: at step s, lane l contributes dim 32*(l/16) + s. The C layout puts one
+ * token's four heads in a lane's four accumulators. Workgroup tile: 16 tokens
+ * x 256 blocks, 64 blocks per wave. */
+__global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const float *pool,
+                                                        float *score, uint32_t n_tok,
+                                                        uint32_t n_blocks, uint32_t stride,
+                                                        uint32_t n_head, uint32_t pos0,
+                                                        uint32_t ratio) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t i16 = lane & 15u, kq = lane >> 4;
+    const uint32_t tok0 = blockIdx.y * 16u;
+    const uint32_t blk0 = blockIdx.x * 256u + wave * 64u;
+    if (blk0 >= n_blocks) return;
+
+    const float *ap[4];
+    bool av[4];
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const uint32_t tok = tok0 + 4u * a + (i16 >> 2), head = i16 & 3u;
+        av[a] = tok < n_tok && head < n_head;
+        ap[a] = q + ((size_t)(av[a] ? tok : 0) * n_head + (av[a] ? head : 0)) * IDX_HD + 32u * kq;
+    }
+    const float *bp[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        uint32_t blk = blk0 + 16u * b + i16;
+        blk = blk < n_blocks ? blk : n_blocks - 1;
+        bp[b] = pool + (size_t)blk * IDX_HD + 32u * kq;
+    }
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+    for (uint32_t kc = 0; kc < 32; kc += 8) {
+        float4 A[4][2], B[4][2];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                A[a][h] = av[a] ? ld_vec((const float4 *)(ap[a] + kc) + h)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) B[b][h] = ld_vec((const float4 *)(bp[b] + kc) + h);
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const float4 &av4 = A[a][s >> 2];
+                const float x = (s & 3) == 0 ? av4.x : (s & 3) == 1 ? av4.y : (s & 3) == 2 ? av4.z : av4.w;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const float4 &bv4 = B[b][s >> 2];
+                    const float y = (s & 3) == 0 ? bv4.x : (s & 3) == 1 ? bv4.y : (s & 3) == 2 ? bv4.z : bv4.w;
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[a][b], 0, 0, 0);
+                }
+            }
+        }
+    }
+    /* lane holds C[4*kq + r][i16]: token tok0 + 4a + kq, head r, block blk0 + 16b + i16 */
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const uint32_t tok = tok0 + 4u * a + kq;
+        if (tok >= n_tok) continue;
+        const uint32_t pos = pos0 + tok;
+        const uint32_t n_vis = ratio ? (pos + 1) / ratio : 0;
+        float *srow = score + (size_t)tok * stride;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const uint32_t blk = blk0 + 16u * b + i16;
+            if (blk >= n_blocks) continue;
+            float s = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; r++) s += fmaxf(acc[a][b][r], 0.f);
+            srow[blk] = blk < n_vis ? s : -1.0e30f;
+        }
+    }
+}
+
+/* --------------------------------------------------------------- topk ---- */
+
+constexpr uint32_t TK_T = 1024;        /* threads per row workgroup */
+constexpr uint32_t TK_KPT = 64;        /* register-resident keys per thread */
+constexpr uint32_t TK_CHUNK = TK_T * TK_KPT;
+constexpr uint32_t TK_MAXK = 512;      /* largest k_blk */
+
+/* Order-preserving uint32 key (src/q4_rocm.cu:7471-7474). */
+__device__ inline uint32_t xkey(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+struct TopkSmem {
+    uint32_t hist[256 * 32]; /* bin-major, 32 copies: lane & 31 picks the copy */
+    uint32_t cg[TK_T], ce[TK_T]; /* per (key row, wave) counts -> exclusive offsets */
+    uint32_t wtot[2][16];
+    uint32_t bins[256];
+    int32_t chosen[TK_MAXK];
+    uint32_t st[4]; /* prefix, above, chunk gt total, chunk eq total */
+};
+
+/* Inclusive prefix sum over the 64 lanes of a wave. */
+__device__ inline uint32_t wave_incl_scan(uint32_t v, uint32_t lane) {
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(v, d);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+__device__ inline uint32_t lanes_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+/* One token row: exact top-`need` blocks by (key desc, index asc), emitted
+ * above-threshold ascending then threshold ties ascending, expanded to sel.
+ * Follows src/q4_rocm.cu:7736-7846 (and the device-position pipeline
+ * :7505-7696, which computes the same list). Keys of row element
+ * e = c*TK_CHUNK + r*TK_T + tid live in key[r] during chunk c. */
+template <bool DEV>
+__global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *sel,
+                                                   uint32_t stride, uint32_t k_blk,
+                                                   uint32_t ratio, uint32_t pos0,
+                                                   uint32_t width, const int32_t *pp) {
+    __shared__ TopkSmem sm;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t pos = (DEV ? (uint32_t)*pp : pos0) + t;
+    const uint32_t n_vis = (pos + 1) / ratio;
+    const uint32_t need = n_vis < k_blk ? n_vis : k_blk;
+    int32_t *out = sel + (size_t)t * width;
+    if (need == n_vis) { /* every complete block fits: the dense prefix */
+        for (uint32_t w = tid; w < width; w += TK_T) out[w] = w <= pos ? (int32_t)w : -1;
+        return;
+    }
+    const float *row = score + (size_t)t * stride;
+    const uint32_t nchunk = (n_vis + TK_CHUNK - 1) / TK_CHUNK;
+    uint32_t key[TK_KPT];
+    /* Elements past n_vis get key 0, the smallest key. Since need <= n_vis
+     * they sort below the need-th largest real key (or tie with it only when
+     * that key is 0), so the radix passes need no validity test; the
+     * compaction checks validity for ties when the threshold is 0. */
+    auto load_chunk = [&](uint32_t c) {
+        const float *src = row + (size_t)c * TK_CHUNK + tid;
+        const uint32_t lim = n_vis - c * TK_CHUNK;
+        if (lim >= TK_CHUNK) {
+#pragma unroll
+            for (uint32_t r = 0; r < TK_KPT; r++) key[r] = xkey(ldg(src + r * TK_T));
+        } else {
+#pragma unroll
+            for (uint32_t r = 0; r < TK_KPT; r++)
+                key[r] = r * TK_T + tid < lim ? xkey(ldg(src + r * TK_T)) : 0u;
+        }
+    };
+    auto valid = [&](uint32_t c, uint32_t r) { return c * TK_CHUNK + r * TK_T + tid < n_vis; };
+    if (nchunk == 1) load_chunk(0);
+
+    if (tid == 0) { sm.st[0] = 0; sm.st[1] = 0; }
+    for (uint32_t pass = 0; pass < 4; pass++) {
+        for (uint32_t i = tid; i < 256 * 32; i += TK_T) sm.hist[i] = 0;
+        __syncthreads();
+        const uint32_t sh = 24u - 8u * pass;
+        const uint32_t pre = sm.st[0];
+        uint32_t *hcopy = sm.hist + (lane & 31u);
+        for (uint32_t c = 0; c < nchunk; c++) {
+            if (nchunk > 1) load_chunk(c);
+#pragma unroll
+            for (uint32_t r = 0; r < TK_KPT; r++) {
+                const uint32_t u = key[r];
+                /* digits above this pass must equal the prefix found so far
+                 * (pass 0: the empty prefix, (u >> 8) >> 24 == 0) */
+                const bool m = ((u >> 8) >> sh) == pre;
+                if (m) atomicAdd(hcopy + ((u >> sh) & 255u) * 32u, 1u);
+            }
+        }
+        __syncthreads();
+        { /* fold the 32 copies: four lanes per bin, eight copies each */
+            const uint32_t bin = tid >> 2, part = tid & 3u;
+            const uint32_t *hp = sm.hist + bin * 32u + part * 8u;
+            uint32_t v = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) v += hp[i];
+            v += __shfl_xor(v, 1);
+            v += __shfl_xor(v, 2);
+            if (part == 0) sm.bins[bin] = v;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            uint32_t cnt[4], lsum = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) { cnt[i] = sm.bins[4 * lane + i]; lsum += cnt[i]; }
+            /* suffix sum over lanes: lanes above this one */
+            uint32_t incl = lsum;
+#pragma unroll
+            for (uint32_t d = 1; d < 64; d <<= 1) {
+                const uint32_t o = __shfl_down(incl, d);
+                if (lane + d < 64) incl += o;
+            }
+            uint32_t acc = incl - lsum;
+            const uint32_t above = sm.st[1];
+            const uint32_t target = need - above;
+#pragma unroll
+            for (int i = 3; i >= 0; i--) {
+                if (acc < target && acc + cnt[i] >= target) {
+                    sm.st[0] = (pre << 8) | (4u * lane + (uint32_t)i);
+                    sm.st[1] = above + acc;
+                }
+                acc += cnt[i];
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t thr = sm.st[0];
+    const uint32_t n_gt = sm.st[1];
+    const uint32_t rem = need - n_gt; /* threshold ties still to take */
+
+    /* Ordered compaction. Element order is (chunk, r, wave, lane). */
+    uint32_t carry_g = 0, carry_e = 0;
+    for (uint32_t c = 0; c < nchunk; c++) {
+        if (nchunk > 1) load_chunk(c);
+#pragma unroll
+        for (uint32_t r = 0; r < TK_KPT; r++) {
+            const uint64_t bg = __ballot(key[r] > thr);
+            const uint64_t be = __ballot((key[r] == thr) & ((thr != 0u) | valid(c, r)));
+            if (lane == 0) {
+                sm.cg[r * 16u + wave] = (uint32_t)__popcll(bg);
+                sm.ce[r * 16u + wave] = (uint32_t)__popcll(be);
+            }
+        }
+        __syncthreads();
+        const uint32_t vg = sm.cg[tid], ve = sm.ce[tid];
+        const uint32_t ig = wave_incl_scan(vg, lane), ie = wave_incl_scan(ve, lane);
+        if (lane == 63) { sm.wtot[0][wave] = ig; sm.wtot[1][wave] = ie; }
+        __syncthreads();
+        uint32_t og = 0, oe = 0, tg = 0, te = 0;
+        for (uint32_t w = 0; w < 16; w++) {
+            const uint32_t a = sm.wtot[0][w], b = sm.wtot[1][w];
+            if (w < wave) { og += a; oe += b; }
+            tg += a;
+            te += b;
+        }
+        sm.cg[tid] = og + ig - vg;
+        sm.ce[tid] = oe + ie - ve;
+        __syncthreads();
+        /* An opaque copy of the threshold keeps the compiler from carrying
+         * the first loop's 128 ballot masks across the scan (VGPR spills). */
+        uint32_t thr2 = thr;
+        asm volatile("" : "+v"(thr2));
+#pragma unroll
+        for (uint32_t r = 0; r < TK_KPT; r++) {
+            const bool gt = key[r] > thr2;
+            const bool eq = (key[r] == thr2) & ((thr2 != 0u) | valid(c, r));
+            const uint64_t bg = __ballot(gt), be = __ballot(eq);
+            const uint32_t e = c * TK_CHUNK + r * TK_T + tid;
+            if (gt) {
+                const uint32_t k = carry_g + sm.cg[r * 16u + wave] + lanes_below(bg);
+                if (k < TK_MAXK) sm.chosen[k] = (int32_t)e;
+            }
+            if (eq) {
+                const uint32_t k = carry_e + sm.ce[r * 16u + wave] + lanes_below(be);
+                if (k < rem && n_gt + k < TK_MAXK) sm.chosen[n_gt + k] = (int32_t)e;
+            }
+        }
+        carry_g += tg;
+        carry_e += te;
+        __syncthreads(); /* cg/ce are rewritten by the next chunk */
+    }
+    /* expansion (src/q4_rocm.cu:7668-7696, 7830-7845) */
+    const uint32_t ncs = need * ratio;
+    for (uint32_t w = tid; w < width; w += TK_T) {
+        int32_t v;
+        if (w < ncs) {
+            const uint32_t i = w / ratio, j = w - i * ratio;
+            v = (int32_t)((uint32_t)sm.chosen[i] * ratio + j);
+        } else {
+            const uint32_t tail = n_vis * ratio + (w - ncs);
+            v = tail <= pos ? (int32_t)tail : -1;
+        }
+        out[w] = v;
+    }
+}
+
+/* --------------------------------------------------------------- prep ---- */
+
+constexpr uint32_t PREP_MAXP = 8; /* pairs per lane: hd <= 1024 */
+
+/* RMSNorm * wn, then RoPE of pairs p < n_rot/2 at position pos, for one
+ * (token, head) row per wave (src/q4_rocm.cu:6229-6289). GATE: the source
+ * row is [x | gate] (2*hd floats) and the gate half is copied to g. Lane l
+ * owns pairs p = l + 64m. In place when src == dst (k_prep). */
+template <bool GATE>
+__global__ __launch_bounds__(256) void qsa_prep_k(const float *src, float *dst, float *g,
+                                                  const float *wn, uint32_t n_heads,
+                                                  uint32_t hd, uint32_t n_rot, int32_t pos0,
+                                                  float base, float eps, uint32_t n_rows,
+                                                  const int32_t *pp) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t rowi = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (rowi >= n_rows) return;
+    const uint32_t t = rowi / n_heads;
+    const int32_t pos = (pp ? *pp : pos0) + (int32_t)t;
+    const float *in = src + (size_t)rowi * hd * (GATE ? 2u : 1u);
+    float *o = dst + (size_t)rowi * hd;
+    const uint32_t np = hd / 2;
+    float2 x[PREP_MAXP];
+    float ss = 0.f;
+#pragma unroll
+    for (uint32_t m = 0; m < PREP_MAXP; m++) {
+        const uint32_t p = lane + 64u * m;
+        x[m] = p < np ? ld_vec((const float2 *)in + p) : make_float2(0.f, 0.f);
+        ss = fmaf(x[m].x, x[m].x, ss);
+        ss = fmaf(x[m].y, x[m].y, ss);
+    }
+    if (GATE) {
+        float *gd = g + (size_t)rowi * hd;
+#pragma unroll
+        for (uint32_t m = 0; m < PREP_MAXP; m++) {
+            const uint32_t p = lane + 64u * m;
+            if (p < np) st_vec((float2 *)gd + p, ld_vec((const float2 *)(in + hd) + p));
+        }
+    }
+    ss = wave_sum(ss);
+    const float scale = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)hd) + eps));
+    const uint32_t nrp = n_rot / 2;
+#pragma unroll
+    for (uint32_t m = 0; m < PREP_MAXP; m++) {
+        const uint32_t p = lane + 64u * m;
+        if (p >= np) continue;
+        const float2 w = wn ? ld_vec((const float2 *)wn + p) : make_float2(1.f, 1.f);
+        float y0 = x[m].x * scale * w.x, y1 = x[m].y * scale * w.y;
+        if (p < nrp) rope_rotate(y0, y1, (float)pos, rope_freq(base, p, nrp));
+        st_vec((float2 *)o + p, make_float2(y0, y1));
+    }
+}
+
+bool prep_launch(const float *src, float *dst, float *g, const float *wn, uint32_t n_heads,
+                 uint32_t hd, uint32_t n_rot, int32_t pos0, float base, float eps,
+                 uint32_t n_tok, const int32_t *pp, const char *what) {
+    if (hd == 0 || (hd & 1u) || hd > 128u * PREP_MAXP || n_rot > hd) {
+        Q4KV_ERR("%s: unsupported hd %u / n_rot %u", what, hd, n_rot);
+        return false;
+    }
+    if (((uintptr_t)src | (uintptr_t)dst | (uintptr_t)g | (uintptr_t)wn) & 7u) {
+        Q4KV_ERR("%s: buffers must be 8-byte aligned", what);
+        return false;
+    }
+    const uint64_t rows = (uint64_t)n_tok * n_heads;
+    if (rows > 0xffffffffull / 4u) return false;
+    (void)hipGetLastError();
+    const uint32_t grid = (uint32_t)((rows + 3u) / 4u);
+    if (g)
+        qsa_prep_k<true><<<grid, 256, 0, q4kv_stream>>>(src, dst, g, wn, n_heads, hd, n_rot,
+                                                         pos0, base, eps, (uint32_t)rows, pp);
+    else
+        qsa_prep_k<false><<<grid, 256, 0, q4kv_stream>>>(src, dst, nullptr, wn, n_heads, hd,
+                                                          n_rot, pos0, base, eps,
+                                                          (uint32_t)rows, pp);
+    return q4kv_launch_ok(what);
+}
+
+} // namespace
+
+/* ------------------------------------------------------------ C ABI ---- */
+
+extern "C" bool q4_hip_qsa_q_prep_n(const float *d_qg, const float *d_wn, float *d_q,
+                                    float *d_g, uint32_t n_head, uint32_t hd, uint32_t n_rot,
+                                    int32_t pos0, float base, float eps, uint32_t n_tok) {
+    if (!q4kv_ok || !d_qg || !d_q || !d_g || n_head == 0 || n_tok == 0) return false;
+    return prep_launch(d_qg, d_q, d_g, d_wn, n_head, hd, n_rot, pos0, base, eps, n_tok,
+                       nullptr, "qsa_q_prep");
+}
+extern "C" bool q4_hip_qsa_q_prep(const float *d_qg, const float *d_wn, float *d_q, float *d_g,
+                                  uint32_t n_head, uint32_t hd, uint32_t n_rot, int32_t pos,
+                                  float base, float eps) {
+    return q4_hip_qsa_q_prep_n(d_qg, d_wn, d_q, d_g, n_head, hd, n_rot, pos, base, eps, 1);
+}
+extern "C" bool q4_hip_qsa_q_prep_d(const float *d_qg, const float *d_wn, float *d_q,
+                                    float *d_g, uint32_t n_head, uint32_t hd, uint32_t n_rot,
+                                    float base, float eps) {
+    if (!q4kv_ok || !q4kv_pos_d || !d_qg || !d_q || !d_g || n_head == 0) return false;
+    return prep_launch(d_qg, d_q, d_g, d_wn, n_head, hd, n_rot, 0, base, eps, 1, q4kv_pos_d,
+                       "qsa_q_prep_d");
+}
+extern "C" bool q4_hip_qsa_k_prep_n(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
+                                    uint32_t n_rot, int32_t pos0, float base, float eps,
+                                    uint32_t n_tok) {
+    if (!q4kv_ok || !d_k || n_kvh == 0 || n_tok == 0) return false;
+    return prep_launch(d_k, d_k, nullptr, d_wn, n_kvh, hd, n_rot, pos0, base, eps, n_tok,
+                       nullptr, "qsa_k_prep");
+}
+extern "C" bool q4_hip_qsa_k_prep(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
+                                  uint32_t n_rot, int32_t pos, float base, float eps) {
+    return q4_hip_qsa_k_prep_n(d_k, d_wn, n_kvh, hd, n_rot, pos, base, eps, 1);
+}
+extern "C" bool q4_hip_qsa_k_prep_d(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
+                                    uint32_t n_rot, float base, float eps) {
+    if (!q4kv_ok || !q4kv_pos_d || !d_k || n_kvh == 0) return false;
+    return prep_launch(d_k, d_k, nullptr, d_wn, n_kvh, hd, n_rot, 0, base, eps, 1, q4kv_pos_d,
+                       "qsa_k_prep_d");
+}
+
+extern "C" bool q4_hip_f32_to_f16_d(void *dst_base, uint32_t stride_elems, const float *src,
+                                    uint64_t n) {
+    if (!q4kv_ok || !q4kv_pos_d || !dst_base || !src || !n) return false;
+    const uint64_t grid = (n + 255u) / 256u;
+    if (grid > 0x7fffffffull) return false;
+    (void)hipGetLastError();
+    f16_at_k<<<(uint32_t)grid, 256, 0, q4kv_stream>>>(src, (__half *)dst_base, stride_elems, n,
+                                                      q4kv_pos_d);
+    return q4kv_launch_ok("f32_to_f16_d");
+}
+
+extern "C" bool q4_hip_qsa_pool(const void *raw_f16, float *pool, const float *wn, uint32_t hd,
+                                uint32_t ratio, uint32_t b0, uint32_t b1, uint32_t n_rot,
+                                float rope_base, float eps) {
+    if (!q4kv_ok || !raw_f16 || !pool || b1 <= b0 || hd != IDX_HD || ratio == 0 || n_rot > hd)
+        return false;
+    if (((uintptr_t)raw_f16 & 3u) || ((uintptr_t)pool & 7u)) {
+        Q4KV_ERR("qsa_pool: raw must be 4-byte and pool 8-byte aligned");
+        return false;
+    }
+    (void)hipGetLastError();
+    const uint32_t nwg = (uint32_t)(((uint64_t)(b1 - b0) + 3u) / 4u);
+    const uint32_t grid = nwg < 8192u ? nwg : 8192u;
+    qsa_pool_k<<<grid, 256, 0, q4kv_stream>>>((const uint32_t *)raw_f16, pool, wn, ratio, b0, b1,
+                                              n_rot, rope_base, eps);
+    return q4kv_launch_ok("qsa_pool");
+}
+extern "C" bool q4_hip_qsa_pool_d(const void *raw_f16, float *pool, const float *wn, uint32_t hd,
+                                  uint32_t ratio, uint32_t n_rot, float rope_base, float eps) {
+    if (!q4kv_ok || !q4kv_pos_d || !raw_f16 || !pool || hd != IDX_HD || ratio == 0 ||
+        n_rot > hd)
+        return false;
+    if (((uintptr_t)raw_f16 & 3u) || ((uintptr_t)pool & 7u)) {
+        Q4KV_ERR("qsa_pool_d: raw must be 4-byte and pool 8-byte aligned");
+        return false;
+    }
+    (void)hipGetLastError();
+    qsa_pool_dk<<<1, 64, 0, q4kv_stream>>>((const uint32_t *)raw_f16, pool, wn, ratio, n_rot,
+                                           rope_base, eps, q4kv_pos_d);
+    return q4kv_launch_ok("qsa_pool_d");
+}
+
+extern "C" bool q4_hip_qsa_score(const float *q, const float *pool, float *score,
+                                 uint32_t n_tok, uint32_t n_blocks, uint32_t stride,
+                                 uint32_t n_head, uint32_t hd, uint32_t pos0, uint32_t ratio) {
+    if (!q4kv_ok || !q || !pool || !score || n_tok == 0 || hd != IDX_HD || n_head == 0 ||
+        n_head > 4)
+        return false;
+    if (n_tok > 1 && n_blocks > stride) {
+        Q4KV_ERR("qsa_score: n_blocks %u exceeds the row stride %u", n_blocks, stride);
+        return false;
+    }
+    if (((uintptr_t)q & 15u) || ((uintptr_t)pool & 15u)) {
+        Q4KV_ERR("qsa_score: q and pool must be 16-byte aligned");
+        return false;
+    }
+    if (n_blocks == 0) return true;
+    (void)hipGetLastError();
+    if (n_tok < 4) {
+        const uint32_t gx = (n_blocks + SC_ROWS_WG - 1) / SC_ROWS_WG;
+        qsa_score_v_k<false><<<dim3(gx, n_tok), 256, 0, q4kv_stream>>>(
+            q, pool, score, n_blocks, stride, n_head, pos0, ratio, nullptr);
+    } else {
+        const uint32_t gx = (n_blocks + 255u) / 256u, gy = (n_tok + 15u) / 16u;
+        qsa_score_mfma_k<<<dim3(gx, gy), 256, 0, q4kv_stream>>>(q, pool, score, n_tok, n_blocks,
+                                                                stride, n_head, pos0, ratio);
+    }
+    return q4kv_launch_ok("qsa_score");
+}
+extern "C" bool q4_hip_qsa_score_d(const float *q, const float *pool, float *score,
+                                   uint32_t stride, uint32_t n_head, uint32_t hd,
+                                   uint32_t ratio) {
+    if (!q4kv_ok || !q4kv_pos_d || !q || !pool || !score || hd != IDX_HD || n_head == 0 ||
+        n_head > 4)
+        return false;
+    if (((uintptr_t)q & 15u) || ((uintptr_t)pool & 15u)) {
+        Q4KV_ERR("qsa_score_d: q and pool must be 16-byte aligned");
+        return false;
+    }
+    if (stride == 0) return true;
+    (void)hipGetLastError();
+    /* Fixed grid sized by the row capacity (graph-capture safe); workgroups
+     * past the device position's visible blocks exit at once. */
+    const uint32_t gx = (stride + SC_ROWS_WG - 1) / SC_ROWS_WG;
+    qsa_score_v_k<true><<<dim3(gx, 1), 256, 0, q4kv_stream>>>(q, pool, score, stride, stride,
+                                                              n_head, 0, ratio, q4kv_pos_d);
+    return q4kv_launch_ok("qsa_score_d");
+}
+
+extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok,
+                                uint32_t n_blocks, uint32_t stride, uint32_t k_blk,
+                                uint32_t ratio, uint32_t pos0, uint32_t width) {
+    (void)n_blocks; /* rows are bounded by each token's visible blocks */
+    if (!q4kv_ok || !score || !sel || n_tok == 0 || k_blk == 0 || k_blk > TK_MAXK ||
+        width == 0 || ratio == 0)
+        return false;
+    (void)hipGetLastError();
+    qsa_topk_k<false><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk, ratio, pos0,
+                                                        width, nullptr);
+    return q4kv_launch_ok("qsa_topk");
+}
+extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride,
+                                  uint32_t k_blk, uint32_t ratio, uint32_t width) {
+    if (!q4kv_ok || !q4kv_pos_d || !score || !sel || k_blk == 0 || k_blk > TK_MAXK ||
+        width == 0 || ratio == 0)
+        return false;
+    (void)stride;
+    (void)hipGetLastError();
+    qsa_topk_k<true><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0, width,
+                                                   q4kv_pos_d);
+    return q4kv_launch_ok("qsa_topk_d");
+}

@@ -90,6 +90,20 @@ SIGNATURES = {
     "q4_hip_f32_to_q8": (_b, [_vp, _vp, _u64]),
     "q4_hip_f32_to_f16": (_b, [_vp, _vp, _u64]),
     "q4_hip_kv_append_d": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, C.c_int]),
+    "q4_hip_qsa_q_prep": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_int32, _f32, _f32]),
+    "q4_hip_qsa_q_prep_n": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_int32, _f32, _f32,
+                                 _u32]),
+    "q4_hip_qsa_q_prep_d": (_b, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _f32]),
+    "q4_hip_qsa_k_prep": (_b, [_vp, _vp, _u32, _u32, _u32, C.c_int32, _f32, _f32]),
+    "q4_hip_qsa_k_prep_n": (_b, [_vp, _vp, _u32, _u32, _u32, C.c_int32, _f32, _f32, _u32]),
+    "q4_hip_qsa_k_prep_d": (_b, [_vp, _vp, _u32, _u32, _u32, _f32, _f32]),
+    "q4_hip_f32_to_f16_d": (_b, [_vp, _u32, _vp, _u64]),
+    "q4_hip_qsa_pool": (_b, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _f32]),
+    "q4_hip_qsa_pool_d": (_b, [_vp, _vp, _vp, _u32, _u32, _u32, _f32, _f32]),
+    "q4_hip_qsa_score": (_b, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "q4_hip_qsa_score_d": (_b, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "q4_hip_qsa_topk": (_b, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "q4_hip_qsa_topk_d": (_b, [_vp, _vp, _u32, _u32, _u32, _u32]),
     "q4_hip_qsa_decode_n": (_b, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
                                  _u32, _f32, C.c_int]),
     "q4_hip_qsa_decode_idx": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,

@@ -42,6 +42,19 @@ class Oracle:
         L.orc_attn.restype = C.c_int
         L.orc_attn.argtypes = [vp, vp, vp, C.c_int, vp, vp, u32, u32, u32, u32, vp, u32,
                                u64, u64, u32, u32, f32, C.c_int, C.c_int]
+        i32 = C.c_int32
+        L.orc_qsa_key.restype = u32
+        L.orc_qsa_key.argtypes = [f32]
+        L.orc_rope_freq.restype = f32
+        L.orc_rope_freq.argtypes = [f32, u32, u32]
+        L.orc_qsa_prep.restype = C.c_int
+        L.orc_qsa_prep.argtypes = [vp, vp, vp, u32, u32, i32, f32, f32]
+        L.orc_qsa_pool.restype = C.c_int
+        L.orc_qsa_pool.argtypes = [vp, vp, vp, u32, u32, u32, u32, u32, f32, f32]
+        L.orc_qsa_score.restype = C.c_int
+        L.orc_qsa_score.argtypes = [vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]
+        L.orc_qsa_topk.restype = C.c_int
+        L.orc_qsa_topk.argtypes = [vp, vp, u32, u32, u32, u32, u32, u32]
         L.orc_check_f16c.restype = u64
         L.orc_check_f16c.argtypes = [u64, u64, u64]
         self.ref = None
@@ -98,3 +111,40 @@ class Oracle:
                                kvh_stride, kv_base, max_kv, float(scale), int(dbl), threads)
         assert rc == 0
         return out
+
+    # --- QSA indexer ----------------------------------------------------------
+    def qsa_prep(self, x, wn, n_rot, pos0, base, eps):
+        """x [n_tok][n_head][hd] -> RMSNorm*wn + RoPE at pos0+t (per head)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        wn = None if wn is None else np.ascontiguousarray(wn, dtype=np.float32)
+        out = np.empty_like(x)
+        n_tok, n_head, hd = x.shape
+        for t in range(n_tok):
+            for h in range(n_head):
+                assert self.lib.orc_qsa_prep(_ptr(x[t, h]), _ptr(out[t, h]), _ptr(wn), hd,
+                                             n_rot, pos0 + t, base, eps) == 0
+        return out
+
+    def qsa_pool(self, raw, pool, wn, hd, ratio, b0, b1, n_rot, base, eps):
+        raw = np.ascontiguousarray(raw, dtype=np.uint16)
+        wn = None if wn is None else np.ascontiguousarray(wn, dtype=np.float32)
+        assert pool.dtype == np.float32 and pool.flags.c_contiguous
+        assert self.lib.orc_qsa_pool(_ptr(raw), _ptr(pool), _ptr(wn), hd, ratio, b0, b1,
+                                     n_rot, base, eps) == 0
+        return pool
+
+    def qsa_score(self, q, pool, n_tok, n_blocks, stride, n_head, hd, pos0, ratio, out=None):
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        pool = np.ascontiguousarray(pool, dtype=np.float32)
+        if out is None:
+            out = np.full((n_tok, stride), np.nan, dtype=np.float32)
+        assert self.lib.orc_qsa_score(_ptr(q), _ptr(pool), _ptr(out), n_tok, n_blocks,
+                                      stride, n_head, hd, pos0, ratio) == 0
+        return out
+
+    def qsa_topk(self, score, n_tok, stride, k_blk, ratio, pos0, width):
+        score = np.ascontiguousarray(score, dtype=np.float32)
+        sel = np.empty((n_tok, width), dtype=np.int32)
+        assert self.lib.orc_qsa_topk(_ptr(score), _ptr(sel), n_tok, stride, k_blk, ratio,
+                                     pos0, width) == 0
+        return sel
