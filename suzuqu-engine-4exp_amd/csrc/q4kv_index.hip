@@ -23,17 +23,22 @@
  *          prefill (>= 4 tokens): fp32 MFMA 16x16x4 with A rows (token, head)
  *          so each lane's four accumulators are one token's four heads and
  *          the relu-sum over heads stays in the lane.
- *   topk   one 1024-thread workgroup per token row: keys live in VGPRs (64 per
- *          thread, 65536 per chunk), four 8-bit radix passes into a 32-way
- *          replicated LDS histogram (no same-address atomics within a
- *          half-wave), then an ordered compaction by wave ballots + one block
- *          scan, then the expansion. Two launches replace the reference's
- *          eleven on the device-position path.
+ *   topk   one 1024-thread workgroup per token row, keys in VGPRs (64 per
+ *          thread). One histogram pass of the distance from the row maximum
+ *          (1/16-octave steps of |score|, 32-way replicated LDS counters so
+ *          a half-wave's atomics hit distinct banks) isolates a small
+ *          candidate set, compacted in index order (LDS atomic-or lane masks
+ *          and one block scan); two exact radix passes run over the
+ *          threshold bin's candidates only. Rows that do not reduce (heavy ties,
+ *          more than 65536 blocks) take four 8-bit radix passes over every
+ *          key. One launch replaces the reference's ten on the
+ *          device-position path.
  */
 #include "q4kv_internal.h"
 #include "q4kv.h"
 
 #include <math.h>
+#include <utility>
 
 namespace {
 
@@ -311,6 +316,10 @@ constexpr uint32_t TK_T = 1024;        /* threads per row workgroup */
 constexpr uint32_t TK_KPT = 64;        /* register-resident keys per thread */
 constexpr uint32_t TK_CHUNK = TK_T * TK_KPT;
 constexpr uint32_t TK_MAXK = 512;      /* largest k_blk */
+constexpr uint32_t TK_CAP = 4096;      /* candidate list capacity */
+constexpr uint32_t TK_DSHIFT = 19;     /* coarse bins: 1/16 octave of |score| */
+constexpr uint32_t TK_DBINS = 512;     /* distance bins from the row maximum */
+constexpr uint32_t TK_CBITS = 10;      /* widest digit of the candidate passes */
 
 /* Order-preserving uint32 key (src/q4_rocm.cu:7471-7474). */
 __device__ inline uint32_t xkey(float f) {
@@ -318,23 +327,86 @@ __device__ inline uint32_t xkey(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+union TopkHist {
+    uint32_t rep[256 * 32];          /* full path: 256 bins x 32 copies */
+    uint32_t dist[TK_DBINS * 32];    /* distance bins x 32 copies */
+    uint32_t cand[1u << TK_CBITS];   /* candidate passes */
+};
 struct TopkSmem {
-    uint32_t hist[256 * 32]; /* bin-major, 32 copies: lane & 31 picks the copy */
-    uint32_t cg[TK_T], ce[TK_T]; /* per (key row, wave) counts -> exclusive offsets */
-    uint32_t wtot[2][16];
-    uint32_t bins[256];
+    TopkHist h;
+    uint32_t cg[TK_T], ce[TK_T];     /* per (key row, wave) counts -> offsets */
+    uint64_t wm[TK_T];               /* per (key row, wave) candidate lane masks */
+    uint32_t ckey[TK_CAP];           /* candidates in index order */
+    int32_t cidx[TK_CAP];
+    uint32_t bins[TK_DBINS];
+    uint32_t wtot[3][16];
     int32_t chosen[TK_MAXK];
-    uint32_t st[4]; /* prefix, above, chunk gt total, chunk eq total */
+    uint32_t st[8];
 };
 
-/* Inclusive prefix sum over the 64 lanes of a wave. */
-__device__ inline uint32_t wave_incl_scan(uint32_t v, uint32_t lane) {
+/* Inclusive prefix sum over the 64 lanes (DPP row shifts + row broadcasts). */
+__device__ inline uint32_t wave_incl_scan(uint32_t x) {
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false); /* row_shr:1 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false); /* row_shr:2 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false); /* row_shr:4 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false); /* row_shr:8 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false); /* row_bcast:15 */
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false); /* row_bcast:31 */
+    return x;
+}
+__device__ inline uint32_t wave_max_u32(uint32_t x) {
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+/* Exclusive prefix sum over the 1024 threads in thread order; *total gets
+ * the sum. Uses wtot[0]; ends with a barrier so wtot may be reused. */
+__device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t *wtot, uint32_t *total) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t inc = wave_incl_scan(v);
+    if (lane == 63) wtot[wave] = inc;
+    __syncthreads();
+    uint32_t pre = 0, tot = 0;
 #pragma unroll
-    for (uint32_t d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_up(v, d);
-        if (lane >= d) v += o;
+    for (uint32_t w = 0; w < 16; w++) {
+        const uint32_t x = wtot[w];
+        pre += w < wave ? x : 0u;
+        tot += x;
     }
+    __syncthreads();
+    *total = tot;
+    return pre + inc - v;
+}
+
+/* The same without the trailing barrier: the caller separates two uses of
+ * one wtot buffer by another barrier. Returns the exclusive prefix. */
+__device__ inline uint32_t block_excl_scan_nb(uint32_t v, uint32_t *wtot) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t inc = wave_incl_scan(v);
+    if (lane == 63) wtot[wave] = inc;
+    __syncthreads();
+    uint32_t pre = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 16; w++) pre += w < wave ? wtot[w] : 0u;
+    return pre + inc - v;
+}
+
+/* Write the wave-uniform value n into lane R of v (v_writelane_b32). */
+template <uint32_t R> __device__ inline uint32_t set_lane(uint32_t v, uint32_t n) {
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(n), "i"(R));
     return v;
+}
+/* f(integral_constant<0>) ... f(integral_constant<N-1>), fully unrolled. */
+template <class F, uint32_t... I>
+__device__ inline void unroll_seq(F &&f, std::integer_sequence<uint32_t, I...>) {
+    (f(std::integral_constant<uint32_t, I>{}), ...);
+}
+template <uint32_t N, class F> __device__ inline void unroll(F &&f) {
+    unroll_seq(f, std::make_integer_sequence<uint32_t, N>{});
 }
 
 __device__ inline uint32_t lanes_below(uint64_t m) {
@@ -344,9 +416,17 @@ __device__ inline uint32_t lanes_below(uint64_t m) {
 
 /* One token row: exact top-`need` blocks by (key desc, index asc), emitted
  * above-threshold ascending then threshold ties ascending, expanded to sel.
- * Follows src/q4_rocm.cu:7736-7846 (and the device-position pipeline
- * :7505-7696, which computes the same list). Keys of row element
- * e = c*TK_CHUNK + r*TK_T + tid live in key[r] during chunk c. */
+ * Same list as src/q4_rocm.cu:7736-7846 (and the device-position pipeline
+ * :7505-7696). Keys of row element e = c*TK_CHUNK + r*TK_T + tid live in
+ * key[r] during chunk c.
+ *
+ * Fast path (rows of <= 65536 blocks): one histogram pass of the distance
+ * from the row maximum finds the bin holding the need-th key; every key in
+ * that bin or nearer is a candidate (typically 1-3 x need). When they fit
+ * in TK_CAP, the candidates are compacted in index order into LDS and the
+ * exact threshold is found by 12-bit radix passes over them alone.
+ * Otherwise (long rows, heavy ties) the full path runs four 8-bit radix
+ * passes over all keys and an ordered compaction of all keys. */
 template <bool DEV>
 __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *sel,
                                                    uint32_t stride, uint32_t k_blk,
@@ -369,7 +449,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
     /* Elements past n_vis get key 0, the smallest key. Since need <= n_vis
      * they sort below the need-th largest real key (or tie with it only when
      * that key is 0), so the radix passes need no validity test; the
-     * compaction checks validity for ties when the threshold is 0. */
+     * compactions check validity where a threshold can be 0. */
     auto load_chunk = [&](uint32_t c) {
         const float *src = row + (size_t)c * TK_CHUNK + tid;
         const uint32_t lim = n_vis - c * TK_CHUNK;
@@ -383,117 +463,250 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         }
     };
     auto valid = [&](uint32_t c, uint32_t r) { return c * TK_CHUNK + r * TK_T + tid < n_vis; };
-    if (nchunk == 1) load_chunk(0);
 
-    if (tid == 0) { sm.st[0] = 0; sm.st[1] = 0; }
-    for (uint32_t pass = 0; pass < 4; pass++) {
-        for (uint32_t i = tid; i < 256 * 32; i += TK_T) sm.hist[i] = 0;
-        __syncthreads();
-        const uint32_t sh = 24u - 8u * pass;
-        const uint32_t pre = sm.st[0];
-        uint32_t *hcopy = sm.hist + (lane & 31u);
-        for (uint32_t c = 0; c < nchunk; c++) {
-            if (nchunk > 1) load_chunk(c);
+    bool fast = nchunk == 1;
+    if (fast) {
+        for (uint32_t i = tid; i < TK_DBINS * 32; i += TK_T) sm.h.dist[i] = 0;
+        sm.wm[tid] = 0;
+        load_chunk(0);
+        /* ---- row maximum (as the loads land) ---- */
+        uint32_t mx = 0;
 #pragma unroll
-            for (uint32_t r = 0; r < TK_KPT; r++) {
-                const uint32_t u = key[r];
-                /* digits above this pass must equal the prefix found so far
-                 * (pass 0: the empty prefix, (u >> 8) >> 24 == 0) */
-                const bool m = ((u >> 8) >> sh) == pre;
-                if (m) atomicAdd(hcopy + ((u >> sh) & 255u) * 32u, 1u);
-            }
-        }
+        for (uint32_t r = 0; r < TK_KPT; r++) mx = max(mx, key[r]);
+        mx = wave_max_u32(mx);
+        if (lane == 0) sm.wtot[1][wave] = mx;
         __syncthreads();
-        { /* fold the 32 copies: four lanes per bin, eight copies each */
-            const uint32_t bin = tid >> 2, part = tid & 3u;
-            const uint32_t *hp = sm.hist + bin * 32u + part * 8u;
+        uint32_t M = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < 16; w++) M = max(M, sm.wtot[1][w]);
+        /* ---- histogram of the distance from the maximum in 1/16-octave
+         * steps of |score| (the keys' bits above bit 19), clamped at 511;
+         * 32 copies keep a half-wave's atomics on distinct banks ---- */
+        const uint32_t Mb = M >> TK_DSHIFT;
+        uint32_t *hc = sm.h.dist + (lane & 31u);
+#pragma unroll
+        for (uint32_t r = 0; r < TK_KPT; r++)
+            atomicAdd(hc + min(Mb - (key[r] >> TK_DSHIFT), TK_DBINS - 1u) * 32u, 1u);
+        __syncthreads();
+        { /* fold the copies: two threads per bin */
+            const uint32_t *hp = sm.h.dist + (tid >> 1) * 32u + (tid & 1u) * 16u;
             uint32_t v = 0;
 #pragma unroll
-            for (int i = 0; i < 8; i++) v += hp[i];
+            for (int i = 0; i < 16; i++) v += hp[i];
             v += __shfl_xor(v, 1);
-            v += __shfl_xor(v, 2);
-            if (part == 0) sm.bins[bin] = v;
+            if ((tid & 1u) == 0) sm.bins[tid >> 1] = v;
         }
         __syncthreads();
-        if (wave == 0) {
-            uint32_t cnt[4], lsum = 0;
+        if (wave == 0) { /* the nearest bin where the count reaches need */
+            uint32_t c[8], s = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) { cnt[i] = sm.bins[4 * lane + i]; lsum += cnt[i]; }
-            /* suffix sum over lanes: lanes above this one */
-            uint32_t incl = lsum;
+            for (int i = 0; i < 8; i++) { c[i] = sm.bins[8u * lane + i]; s += c[i]; }
+            uint32_t acc = wave_incl_scan(s) - s;
 #pragma unroll
-            for (uint32_t d = 1; d < 64; d <<= 1) {
-                const uint32_t o = __shfl_down(incl, d);
-                if (lane + d < 64) incl += o;
-            }
-            uint32_t acc = incl - lsum;
-            const uint32_t above = sm.st[1];
-            const uint32_t target = need - above;
-#pragma unroll
-            for (int i = 3; i >= 0; i--) {
-                if (acc < target && acc + cnt[i] >= target) {
-                    sm.st[0] = (pre << 8) | (4u * lane + (uint32_t)i);
-                    sm.st[1] = above + acc;
+            for (int i = 0; i < 8; i++) {
+                if (acc < need && acc + c[i] >= need) {
+                    sm.st[0] = 8u * lane + i; /* bin B */
+                    sm.st[1] = acc;           /* keys in nearer bins: selected */
+                    sm.st[2] = acc + c[i];    /* candidates: bins <= B */
                 }
-                acc += cnt[i];
+                acc += c[i];
             }
         }
         __syncthreads();
+        const uint32_t B = sm.st[0], above = sm.st[1], ncand = sm.st[2];
+        /* the clamped last bin and the padding keys' bin take the full path */
+        fast = B < min(Mb, TK_DBINS - 1u) && ncand <= TK_CAP;
+        const uint32_t Kc = (Mb - B) << TK_DSHIFT; /* candidates: key >= Kc */
+        if (fast) {
+            /* ---- ordered compaction of the candidates: each lane's 64-bit
+             * row mask, the (row, wave) lane masks by LDS atomic-or, one
+             * block scan, then a loop over each lane's few candidates
+             * (the full key is fetched again from the row, an L2 hit) ---- */
+            uint32_t mlo = 0, mhi = 0;
+#pragma unroll
+            for (uint32_t r = 0; r < 32; r++) mlo |= key[r] >= Kc ? 1u << r : 0u;
+#pragma unroll
+            for (uint32_t r = 0; r < 32; r++) mhi |= key[32 + r] >= Kc ? 1u << r : 0u;
+            const uint64_t mine0 = ((uint64_t)mhi << 32) | mlo;
+            for (uint64_t m = mine0; m; m &= m - 1ull)
+                atomicOr(&sm.wm[(uint32_t)__builtin_ctzll(m) * 16u + wave], 1ull << lane);
+            __syncthreads();
+            uint32_t tot;
+            const uint32_t off = block_excl_scan((uint32_t)__popcll(sm.wm[tid]), sm.wtot[0], &tot);
+            sm.cg[tid] = off;
+            for (uint32_t i = tid; i < (1u << TK_CBITS); i += TK_T) sm.h.cand[i] = 0;
+            __syncthreads();
+            const uint64_t below = (1ull << lane) - 1ull;
+            for (uint64_t m = mine0; m; m &= m - 1ull) {
+                const uint32_t r = (uint32_t)__builtin_ctzll(m);
+                const uint32_t j = r * 16u + wave;
+                const uint32_t i = sm.cg[j] + (uint32_t)__popcll(sm.wm[j] & below);
+                const uint32_t e = r * TK_T + tid;
+                sm.ckey[i] = xkey(ldg(row + e));
+                sm.cidx[i] = (int32_t)e;
+            }
+            __syncthreads();
+            /* ---- exact threshold inside bin B: its keys share the bits above
+             * bit 19; two radix passes (10 + 9 bits) over those candidates ---- */
+            const uint32_t kb = Kc >> TK_DSHIFT;
+            uint32_t pre = 0, gt = above;
+            for (uint32_t pass = 0; pass < 2; pass++) {
+                const uint32_t lo = pass == 0 ? 9u : 0u, wbits = pass == 0 ? 10u : 9u;
+                const uint32_t nd = 1u << wbits;
+                for (uint32_t i = tid; i < ncand; i += TK_T) {
+                    const uint32_t u = sm.ckey[i];
+                    const uint32_t v = u & ((1u << TK_DSHIFT) - 1u);
+                    if ((u >> TK_DSHIFT) == kb && (pass == 0 || (v >> 9) == pre))
+                        atomicAdd(&sm.h.cand[(v >> lo) & (nd - 1u)], 1u);
+                }
+                __syncthreads();
+                /* thread t owns digit nd-1-t (descending) */
+                const int d = (int)nd - 1 - (int)tid;
+                const uint32_t c = d >= 0 ? sm.h.cand[d] : 0u;
+                const uint32_t acc = block_excl_scan_nb(c, sm.wtot[pass]);
+                const uint32_t target = need - gt;
+                if (acc < target && acc + c >= target) {
+                    sm.st[4 + 2 * pass] = (uint32_t)d;
+                    sm.st[5 + 2 * pass] = acc;
+                }
+                __syncthreads();
+                if (d >= 0) sm.h.cand[d] = 0;
+                pre = pass == 0 ? sm.st[4] : (pre << 9) | sm.st[6];
+                gt += sm.st[5 + 2 * pass];
+                __syncthreads();
+            }
+            const uint32_t thr = Kc | pre;
+            const uint32_t n_gt = gt, rem = need - n_gt;
+            /* ---- ordered output over the index-ordered candidates ---- */
+            uint32_t g = 0, e = 0;
+            const uint32_t i0 = 4u * tid;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t i = i0 + j;
+                if (i < ncand) {
+                    g += sm.ckey[i] > thr;
+                    e += sm.ckey[i] == thr;
+                }
+            }
+            const uint32_t pk = block_excl_scan_nb(g | (e << 16), sm.wtot[2]);
+            uint32_t og = pk & 0xffffu, oe = pk >> 16;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                const uint32_t i = i0 + j;
+                if (i < ncand) {
+                    const uint32_t u = sm.ckey[i];
+                    if (u > thr) {
+                        if (og < TK_MAXK) sm.chosen[og] = sm.cidx[i];
+                        og++;
+                    } else if (u == thr) {
+                        if (oe < rem && n_gt + oe < TK_MAXK) sm.chosen[n_gt + oe] = sm.cidx[i];
+                        oe++;
+                    }
+                }
+            }
+            __syncthreads();
+        }
     }
-    const uint32_t thr = sm.st[0];
-    const uint32_t n_gt = sm.st[1];
-    const uint32_t rem = need - n_gt; /* threshold ties still to take */
-
-    /* Ordered compaction. Element order is (chunk, r, wave, lane). */
-    uint32_t carry_g = 0, carry_e = 0;
-    for (uint32_t c = 0; c < nchunk; c++) {
-        if (nchunk > 1) load_chunk(c);
+    if (!fast) {
+        /* ---- full path: four 8-bit radix passes over every key ---- */
+        if (tid == 0) { sm.st[4] = 0; sm.st[5] = 0; }
+        for (uint32_t pass = 0; pass < 4; pass++) {
+            for (uint32_t i = tid; i < 256 * 32; i += TK_T) sm.h.rep[i] = 0;
+            __syncthreads();
+            const uint32_t sh = 24u - 8u * pass;
+            const uint32_t pre = sm.st[4];
+            uint32_t *hcopy = sm.h.rep + (lane & 31u);
+            for (uint32_t c = 0; c < nchunk; c++) {
+                if (nchunk > 1) load_chunk(c);
 #pragma unroll
-        for (uint32_t r = 0; r < TK_KPT; r++) {
-            const uint64_t bg = __ballot(key[r] > thr);
-            const uint64_t be = __ballot((key[r] == thr) & ((thr != 0u) | valid(c, r)));
-            if (lane == 0) {
-                sm.cg[r * 16u + wave] = (uint32_t)__popcll(bg);
-                sm.ce[r * 16u + wave] = (uint32_t)__popcll(be);
+                for (uint32_t r = 0; r < TK_KPT; r++) {
+                    const uint32_t u = key[r];
+                    /* digits above this pass must equal the prefix found so
+                     * far (pass 0: the empty prefix, (u >> 8) >> 24 == 0) */
+                    if (((u >> 8) >> sh) == pre) atomicAdd(hcopy + ((u >> sh) & 255u) * 32u, 1u);
+                }
             }
-        }
-        __syncthreads();
-        const uint32_t vg = sm.cg[tid], ve = sm.ce[tid];
-        const uint32_t ig = wave_incl_scan(vg, lane), ie = wave_incl_scan(ve, lane);
-        if (lane == 63) { sm.wtot[0][wave] = ig; sm.wtot[1][wave] = ie; }
-        __syncthreads();
-        uint32_t og = 0, oe = 0, tg = 0, te = 0;
-        for (uint32_t w = 0; w < 16; w++) {
-            const uint32_t a = sm.wtot[0][w], b = sm.wtot[1][w];
-            if (w < wave) { og += a; oe += b; }
-            tg += a;
-            te += b;
-        }
-        sm.cg[tid] = og + ig - vg;
-        sm.ce[tid] = oe + ie - ve;
-        __syncthreads();
-        /* An opaque copy of the threshold keeps the compiler from carrying
-         * the first loop's 128 ballot masks across the scan (VGPR spills). */
-        uint32_t thr2 = thr;
-        asm volatile("" : "+v"(thr2));
+            __syncthreads();
+            { /* fold the 32 copies: four lanes per bin, eight copies each */
+                const uint32_t bin = tid >> 2, part = tid & 3u;
+                const uint32_t *hp = sm.h.rep + bin * 32u + part * 8u;
+                uint32_t v = 0;
 #pragma unroll
-        for (uint32_t r = 0; r < TK_KPT; r++) {
-            const bool gt = key[r] > thr2;
-            const bool eq = (key[r] == thr2) & ((thr2 != 0u) | valid(c, r));
-            const uint64_t bg = __ballot(gt), be = __ballot(eq);
-            const uint32_t e = c * TK_CHUNK + r * TK_T + tid;
-            if (gt) {
-                const uint32_t k = carry_g + sm.cg[r * 16u + wave] + lanes_below(bg);
-                if (k < TK_MAXK) sm.chosen[k] = (int32_t)e;
+                for (int i = 0; i < 8; i++) v += hp[i];
+                v += __shfl_xor(v, 1);
+                v += __shfl_xor(v, 2);
+                if (part == 0) sm.bins[bin] = v;
             }
-            if (eq) {
-                const uint32_t k = carry_e + sm.ce[r * 16u + wave] + lanes_below(be);
-                if (k < rem && n_gt + k < TK_MAXK) sm.chosen[n_gt + k] = (int32_t)e;
+            __syncthreads();
+            if (wave == 0) { /* digit where the count from the top reaches the target */
+                uint32_t c[4], s = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) { c[i] = sm.bins[255u - 4u * lane - i]; s += c[i]; }
+                uint32_t acc = wave_incl_scan(s) - s;
+                const uint32_t above = sm.st[5];
+                const uint32_t target = need - above;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (acc < target && acc + c[i] >= target) {
+                        sm.st[4] = (pre << 8) | (255u - 4u * lane - (uint32_t)i);
+                        sm.st[5] = above + acc;
+                    }
+                    acc += c[i];
+                }
             }
+            __syncthreads();
         }
-        carry_g += tg;
-        carry_e += te;
-        __syncthreads(); /* cg/ce are rewritten by the next chunk */
+        const uint32_t thr = sm.st[4];
+        const uint32_t n_gt = sm.st[5];
+        const uint32_t rem = need - n_gt; /* threshold ties still to take */
+        /* ordered compaction; element order is (chunk, r, wave, lane) */
+        uint32_t carry_g = 0, carry_e = 0;
+        for (uint32_t c = 0; c < nchunk; c++) {
+            if (nchunk > 1) load_chunk(c);
+            uint32_t gv = 0, ev = 0;
+            unroll<TK_KPT>([&](auto rc) {
+                constexpr uint32_t r = rc;
+                const uint32_t ng = (uint32_t)__popcll(__ballot(key[r] > thr));
+                const uint32_t ne = (uint32_t)__popcll(
+                    __ballot((key[r] == thr) & ((thr != 0u) | valid(c, r))));
+                gv = set_lane<r>(gv, ng);
+                ev = set_lane<r>(ev, ne);
+            });
+            sm.cg[lane * 16u + wave] = gv;
+            sm.ce[lane * 16u + wave] = ev;
+            __syncthreads();
+            uint32_t tg, te;
+            const uint32_t og = block_excl_scan(sm.cg[tid], sm.wtot[0], &tg);
+            const uint32_t oe = block_excl_scan(sm.ce[tid], sm.wtot[1], &te);
+            sm.cg[tid] = og;
+            sm.ce[tid] = oe;
+            __syncthreads();
+            const uint32_t gov = sm.cg[lane * 16u + wave], eov = sm.ce[lane * 16u + wave];
+            uint32_t thr2 = thr;
+            asm volatile("" : "+v"(thr2)); /* do not carry the first loop's masks */
+#pragma unroll
+            for (uint32_t r = 0; r < TK_KPT; r++) {
+                const bool gt = key[r] > thr2;
+                const bool eq = (key[r] == thr2) & ((thr2 != 0u) | valid(c, r));
+                const uint64_t bg = __ballot(gt), be = __ballot(eq);
+                const uint32_t e = c * TK_CHUNK + r * TK_T + tid;
+                if (bg) {
+                    const uint32_t k = carry_g +
+                                       (uint32_t)__builtin_amdgcn_readlane((int)gov, (int)r) +
+                                       lanes_below(bg);
+                    if (gt && k < TK_MAXK) sm.chosen[k] = (int32_t)e;
+                }
+                if (be) {
+                    const uint32_t k = carry_e +
+                                       (uint32_t)__builtin_amdgcn_readlane((int)eov, (int)r) +
+                                       lanes_below(be);
+                    if (eq && k < rem && n_gt + k < TK_MAXK) sm.chosen[n_gt + k] = (int32_t)e;
+                }
+            }
+            carry_g += tg;
+            carry_e += te;
+            __syncthreads(); /* cg/ce are rewritten by the next chunk */
+        }
     }
     /* expansion (src/q4_rocm.cu:7668-7696, 7830-7845) */
     const uint32_t ncs = need * ratio;

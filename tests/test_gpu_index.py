@@ -24,6 +24,13 @@ def _score_rows(rng, n_vis):
     yield "random", rng.standard_normal(n_vis).astype(np.float32)
     yield "relu-sums", np.maximum(rng.standard_normal(n_vis) * 4, 0).astype(np.float32)
     yield "ties", np.round(rng.standard_normal(n_vis) * 3).astype(np.float32)
+    # a few ties around the threshold, with a small candidate set
+    yield "near-ties", (np.round(rng.standard_normal(n_vis) * 300) / 300).astype(np.float32)
+    # top values far apart (wide candidate range, several radix passes)
+    w = rng.standard_normal(n_vis).astype(np.float32)
+    w[rng.integers(0, n_vis, 300)] = 1e30
+    w[rng.integers(0, n_vis, 300)] = -1e-30
+    yield "wide", w
     z = np.zeros(n_vis, np.float32)
     z[rng.integers(0, n_vis, n_vis // 3)] = -0.0
     z[rng.integers(0, n_vis, 40)] = 1.0
