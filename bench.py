@@ -519,6 +519,98 @@ def config4(b, steps=100, sets=4, layers=4):
 
 
 
+IDX_RATIO, IDX_KBLK, IDX_HEADS, IDX_DIM = 4, 512, 4, 128
+IDX_ROT, IDX_BASE, IDX_EPS = 64, 1.0e7, 1.0e-6
+
+
+def config_indexer(b, steps=100, layers=12):
+    """QSA indexer of the decode step at a full 262144-token context
+    (src/q4_fwd.c:895-925): per layer the raw indexer key store, the pooling
+    of the block it completes, the indexer query's RMSNorm + RoPE, the scores
+    of all 65536 visible blocks and the exact top-512 selection expanded to
+    2051 positions. One graph per step covers `layers` layers, each with its
+    own 64 MiB fp16 key buffer and 32 MiB pool, so the pools (403 MB) stream
+    from HBM. Also times the prefill pool rebuild of one layer."""
+    rt, lib = b.rt, b.lib
+    max_blocks = CTX // IDX_RATIO
+    pos = CTX - 1
+    raws, pools, scs, sels, qs, ks = [], [], [], [], [], []
+    tmp = rt.alloc(CTX * IDX_DIM * 4)
+    wn = rt.alloc(IDX_DIM * 4)
+    b.gen(wn, IDX_DIM, 77)
+    for li in range(layers):
+        raw = rt.alloc(CTX * IDX_DIM * 2)
+        b.gen(tmp, CTX * IDX_DIM, 9000 + li)
+        assert lib.q4_hip_f32_to_f16(raw, tmp, CTX * IDX_DIM)
+        raws.append(raw)
+        pools.append(rt.alloc(max_blocks * IDX_DIM * 4))
+        scs.append(rt.alloc(max_blocks * 4))
+        sels.append(rt.alloc(WIDTH * 4))
+        q = rt.alloc(IDX_HEADS * IDX_DIM * 4)
+        b.gen(q, IDX_HEADS * IDX_DIM, 9100 + li)
+        qs.append(q)
+        k = rt.alloc(IDX_DIM * 4)
+        b.gen(k, IDX_DIM, 9200 + li)
+        ks.append(k)
+    rt.sync()
+    rt.free(tmp)
+    # prefill-style rebuild of every complete block (timed on one layer)
+    for li in range(layers):
+        assert lib.q4_hip_qsa_pool(raws[li], pools[li], wn, IDX_DIM, IDX_RATIO, 0, max_blocks,
+                                   IDX_ROT, IDX_BASE, IDX_EPS)
+    rt.sync()
+    t0 = time.perf_counter()
+    reps = 10
+    for _ in range(reps):
+        assert lib.q4_hip_qsa_pool(raws[0], pools[0], wn, IDX_DIM, IDX_RATIO, 0, max_blocks,
+                                   IDX_ROT, IDX_BASE, IDX_EPS)
+    rt.sync()
+    t_pool = (time.perf_counter() - t0) / reps
+    lib.q4_hip_pos_push(pos)
+    rt.sync()
+
+    def step(parts):
+        ok = True
+        for li in range(layers):
+            if "store" in parts:
+                ok &= lib.q4_hip_f32_to_f16_d(raws[li], IDX_DIM, ks[li], IDX_DIM)
+                ok &= lib.q4_hip_qsa_pool_d(raws[li], pools[li], wn, IDX_DIM, IDX_RATIO,
+                                            IDX_ROT, IDX_BASE, IDX_EPS)
+            if "prep" in parts:
+                ok &= lib.q4_hip_qsa_k_prep_d(qs[li], wn, IDX_HEADS, IDX_DIM, IDX_ROT,
+                                              IDX_BASE, IDX_EPS)
+            if "fused" in parts:
+                ok &= lib.q4_hip_qsa_index_score_d(raws[li], pools[li], wn, ks[li], qs[li], wn,
+                                                   scs[li], max_blocks, IDX_HEADS, IDX_DIM,
+                                                   IDX_RATIO, IDX_ROT, IDX_BASE, IDX_EPS)
+            if "score" in parts:
+                ok &= lib.q4_hip_qsa_score_d(qs[li], pools[li], scs[li], max_blocks, IDX_HEADS,
+                                             IDX_DIM, IDX_RATIO)
+            if "topk" in parts:
+                ok &= lib.q4_hip_qsa_topk_d(scs[li], sels[li], max_blocks, IDX_KBLK, IDX_RATIO,
+                                            WIDTH)
+        return ok
+
+    out = {"what": f"decode indexer, {layers} layers x 65536 visible blocks (ctx {CTX}), "
+                   "4 heads x 128 dims, top-512 of 4-position blocks -> 2051 positions",
+           "launches_per_layer": {"full": 5, "fused": 2}}
+    for name, parts in (("full", ("store", "prep", "score", "topk")), ("score", ("score",)),
+                        ("topk", ("topk",)), ("fused", ("fused", "topk"))):
+        graphs = _graphs(lib, lambda r: step(parts), 2)
+        t = _time_graphs(b, graphs, steps) / layers
+        out[f"{name}_us_per_layer"] = round(t * 1e6, 3)
+    score_b = max_blocks * (IDX_DIM * 4 + 4) + IDX_HEADS * IDX_DIM * 4
+    out["score_bytes_per_layer"] = score_b
+    out["score_gbs"] = round(score_b / (out["score_us_per_layer"] * 1e-6) / 1e9, 1)
+    out["score_pct_of_peak"] = round(100 * out["score_gbs"] / PEAK_GBS, 2)
+    out["pool_rebuild_ms"] = round(t_pool * 1e3, 3)
+    pool_b = CTX * IDX_DIM * 2 + max_blocks * IDX_DIM * 4
+    out["pool_rebuild_gbs"] = round(pool_b / t_pool / 1e9, 1)
+    for p_ in raws + pools + scs + sels + qs + ks + [wn]:
+        rt.free(p_)
+    return out
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -568,7 +660,8 @@ def main():
     configs = None
     if args.configs:
         configs = {"config2_batched_decode": config2(b), "config3_chunked_prefill": config3(b),
-                   "config4_widths_restore": config4(b)}
+                   "config4_widths_restore": config4(b),
+                   "indexer_decode": config_indexer(b)}
     threads = min(16, os.cpu_count() or 1)
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
     head = "batched" if "batched" in res else "sequential"

@@ -188,6 +188,17 @@ typedef struct {
     uint32_t reserved;
 } q4kv_append_desc;
 
+/* The decode indexer step in one launch (src/q4_fwd.c:904-916 fused): the
+ * effect of q4_hip_f32_to_f16_d(raw_f16, hd, k_new, hd), then
+ * q4_hip_qsa_pool_d(raw_f16, pool, wn_k, hd, ratio, n_rot, rope_base, eps),
+ * then q4_hip_qsa_k_prep_d on a copy of q with wn_q, then
+ * q4_hip_qsa_score_d(that copy, pool, score, stride, n_head, hd, ratio):
+ * the same raw row, pool rows and scores. q itself is not modified. */
+bool q4_hip_qsa_index_score_d(void *raw_f16, float *pool, const float *wn_k, const float *k_new,
+                              const float *q, const float *wn_q, float *score, uint32_t stride,
+                              uint32_t n_head, uint32_t hd, uint32_t ratio, uint32_t n_rot,
+                              float rope_base, float eps);
+
 /* Append into n_desc caches in one launch (the per-layer
  * q4_hip_kv_append_d of a decode step, batched). */
 bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc, uint32_t n,

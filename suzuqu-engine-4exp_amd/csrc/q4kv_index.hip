@@ -89,11 +89,14 @@ __device__ inline void rope_rotate(float &x0, float &x1, float pos_f, float freq
 /* --------------------------------------------------------------- pool ---- */
 
 /* Pool block b into pool[b][0..128): mean of `ratio` fp16 rows, RMSNorm * wn,
- * RoPE at position b*ratio. One wave; lane l owns dims 2l, 2l+1.
+ * RoPE at position b*ratio. One wave; lane l owns dims 2l, 2l+1. When last
+ * is non-zero it replaces the block's last raw row (fp16 pair bits), the row
+ * that is being stored in the same launch. Returns this lane's pooled pair.
  * src/q4_rocm.cu:7366-7401. */
-__device__ inline void pool_block(const uint32_t *raw2, float *pool, const float *wn,
-                                  uint32_t ratio, uint32_t b, uint32_t n_rot, float freq,
-                                  float eps, uint32_t lane) {
+__device__ __attribute__((always_inline)) inline float2 pool_block(const uint32_t *raw2, float *pool, const float *wn,
+                                    uint32_t ratio, uint32_t b, uint32_t n_rot, float freq,
+                                    float eps, uint32_t lane, bool use_last = false,
+                                    uint32_t last = 0) {
     const uint32_t *src = raw2 + (size_t)b * ratio * (IDX_HD / 2) + lane;
     float s0 = 0.f, s1 = 0.f;
     uint32_t j = 0;
@@ -101,6 +104,7 @@ __device__ inline void pool_block(const uint32_t *raw2, float *pool, const float
         uint32_t h[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) h[i] = ldg(src + (size_t)(j + i) * (IDX_HD / 2));
+        if (use_last && j + 4 == ratio) h[3] = last;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             s0 += __half2float(__ushort_as_half((unsigned short)(h[i] & 0xffffu)));
@@ -108,7 +112,8 @@ __device__ inline void pool_block(const uint32_t *raw2, float *pool, const float
         }
     }
     for (; j < ratio; j++) {
-        const uint32_t h = ldg(src + (size_t)j * (IDX_HD / 2));
+        uint32_t h = ldg(src + (size_t)j * (IDX_HD / 2));
+        if (use_last && j + 1 == ratio) h = last;
         s0 += __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
         s1 += __half2float(__ushort_as_half((unsigned short)(h >> 16)));
     }
@@ -120,6 +125,7 @@ __device__ inline void pool_block(const uint32_t *raw2, float *pool, const float
     v1 = v1 * inv * w1;
     if (2 * lane < n_rot) rope_rotate(v0, v1, (float)(b * ratio), freq);
     st_vec((float2 *)(pool + (size_t)b * IDX_HD) + lane, make_float2(v0, v1));
+    return make_float2(v0, v1);
 }
 
 __global__ __launch_bounds__(256) void qsa_pool_k(const uint32_t *raw2, float *pool,
@@ -160,36 +166,15 @@ __global__ __launch_bounds__(256) void f16_at_k(const float *src, __half *dst0, 
 
 constexpr uint32_t SC_ROWS_WG = 64; /* 4 waves x 2 x 8 rows */
 
-/* Streaming block scores for few tokens (decode: one token at the device
- * position). Token t = blockIdx.y; rows b < n_vis get sum_h relu(q_h . pool_b),
- * n_vis <= b < n_blocks get -1e30 (src/q4_rocm.cu:7412-7445, 7476-7503).
- * DEV: the device position bounds the rows written to b < n_vis. */
-template <bool DEV>
-__global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float *pool,
-                                                     float *score, uint32_t n_blocks,
-                                                     uint32_t stride, uint32_t n_head,
-                                                     uint32_t pos0, uint32_t ratio,
-                                                     const int32_t *pp) {
-    const uint32_t t = blockIdx.y;
-    const uint32_t pos = (DEV ? (uint32_t)*pp : pos0) + t;
-    const uint32_t n_vis = ratio ? (pos + 1) / ratio : 0;
-    if (DEV) n_blocks = n_vis;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+/* The scores of rows rb + [0, 64) (and further grid strides) of one token:
+ * eight lanes per row, lane g holding dims {32i + 4g .. +3 : i < 4} of each
+ * query in qr. Row b_new, when in range, is taken from nr (this lane's dims
+ * of the pooled row this launch produced) instead of the pool. */
+__device__ __attribute__((always_inline)) inline void score_rows(const float4 (&qr)[4][4], const float *pool, float *srow,
+                                  uint32_t rb, uint32_t n_blocks, uint32_t n_vis,
+                                  uint32_t lane, uint32_t wave, float4 nr0, float4 nr1,
+                                  float4 nr2, float4 nr3, uint32_t b_new) {
     const uint32_t g = lane & 7u, rsub = lane >> 3;
-    uint32_t rb = blockIdx.x * SC_ROWS_WG;
-    if (rb >= n_blocks) return;
-
-    /* lane g of a row group holds dims {32i + 4g .. +3 : i < 4} of each query */
-    float4 qr[4][4];
-#pragma unroll
-    for (int h = 0; h < 4; h++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            qr[h][i] = (uint32_t)h < n_head
-                           ? ld_vec((const float4 *)(q + ((size_t)t * n_head + h) * IDX_HD +
-                                                  32 * i + 4 * g))
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-    float *srow = score + (size_t)t * stride;
     const uint32_t rlast = n_vis ? n_vis - 1 : 0;
     for (; rb < n_blocks; rb += gridDim.x * SC_ROWS_WG) {
         float4 p[2][4];
@@ -201,6 +186,12 @@ __global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float
             const float4 *src = (const float4 *)(pool + (size_t)r * IDX_HD) + g;
 #pragma unroll
             for (int i = 0; i < 4; i++) p[u][i] = ld_vec(src + 8 * i);
+            if (row[u] == b_new) {
+                p[u][0] = nr0;
+                p[u][1] = nr1;
+                p[u][2] = nr2;
+                p[u][3] = nr3;
+            }
         }
 #pragma unroll
         for (int u = 0; u < 2; u++) {
@@ -220,6 +211,104 @@ __global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float
             if (g == 0 && row[u] < n_blocks) srow[row[u]] = row[u] < n_vis ? s : -1.0e30f;
         }
     }
+}
+
+/* Streaming block scores for few tokens (decode: one token at the device
+ * position). Token t = blockIdx.y; rows b < n_vis get sum_h relu(q_h . pool_b),
+ * n_vis <= b < n_blocks get -1e30 (src/q4_rocm.cu:7412-7445, 7476-7503).
+ * DEV: the device position bounds the rows written to b < n_vis. */
+template <bool DEV>
+__global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float *pool,
+                                                     float *score, uint32_t n_blocks,
+                                                     uint32_t stride, uint32_t n_head,
+                                                     uint32_t pos0, uint32_t ratio,
+                                                     const int32_t *pp) {
+    const uint32_t t = blockIdx.y;
+    const uint32_t pos = (DEV ? (uint32_t)*pp : pos0) + t;
+    const uint32_t n_vis = ratio ? (pos + 1) / ratio : 0;
+    if (DEV) n_blocks = n_vis;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t g = lane & 7u;
+    uint32_t rb = blockIdx.x * SC_ROWS_WG;
+    if (rb >= n_blocks) return;
+
+    /* lane g of a row group holds dims {32i + 4g .. +3 : i < 4} of each query */
+    float4 qr[4][4];
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            qr[h][i] = (uint32_t)h < n_head
+                           ? ld_vec((const float4 *)(q + ((size_t)t * n_head + h) * IDX_HD +
+                                                  32 * i + 4 * g))
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    score_rows(qr, pool, score + (size_t)t * stride, rb, n_blocks, n_vis, lane, wave, z, z, z, z,
+               0xffffffffu);
+}
+
+/* The decode indexer step in one launch (no reference counterpart; it is
+ * q4_hip_f32_to_f16_d + q4_hip_qsa_pool_d + q4_hip_qsa_k_prep_d +
+ * q4_hip_qsa_score_d of src/q4_fwd.c:904-916, fused): workgroup 0 stores
+ * the new raw key at the device position; every workgroup prepares the
+ * indexer queries itself (RMSNorm * wn_q + RoPE at pos, one wave per head,
+ * into LDS); the workgroup whose rows hold the block this position
+ * completes pools it (with the new key's fp16 row in place of the stored
+ * one) and writes it to the pool; then every workgroup scores its 64 rows.
+ * q is read, not modified. */
+__global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float *pool,
+                                                          const float *wn_k, const float *k_new,
+                                                          const float *q, const float *wn_q,
+                                                          float *score, uint32_t n_head,
+                                                          uint32_t ratio, uint32_t n_rot,
+                                                          float base, float eps,
+                                                          const int32_t *pp) {
+    __shared__ float qs[4][IDX_HD];
+    __shared__ float new_row[IDX_HD];
+    const uint32_t pos = (uint32_t)*pp;
+    const uint32_t n_vis = (pos + 1) / ratio;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t rb = blockIdx.x * SC_ROWS_WG;
+    /* fp16 pair of the new key this lane owns (dims 2*lane, 2*lane+1) */
+    const float2 kn = ld_vec((const float2 *)k_new + lane);
+    const uint32_t kh = (uint32_t)__half_as_ushort(__float2half_rn(kn.x)) |
+                        ((uint32_t)__half_as_ushort(__float2half_rn(kn.y)) << 16);
+    if (blockIdx.x == 0 && wave == 0) stg(raw2 + (size_t)pos * (IDX_HD / 2) + lane, kh);
+    if (rb >= n_vis) return;
+    const float freq = 2 * lane < n_rot ? rope_freq(base, lane, n_rot / 2) : 0.f;
+    /* indexer queries: wave h prepares head h (qsa_prep_k's arithmetic) */
+    {
+        float2 x = make_float2(0.f, 0.f);
+        if (wave < n_head) x = ld_vec((const float2 *)(q + wave * IDX_HD) + lane);
+        float ss = fmaf(x.x, x.x, 0.f);
+        ss = fmaf(x.y, x.y, ss);
+        ss = wave_sum(ss);
+        const float scale = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)IDX_HD) + eps));
+        const float2 w = wn_q ? ld_vec((const float2 *)wn_q + lane) : make_float2(1.f, 1.f);
+        float y0 = x.x * scale * w.x, y1 = x.y * scale * w.y;
+        if (2 * lane < n_rot) rope_rotate(y0, y1, (float)pos, freq);
+        if (wave >= n_head) y0 = y1 = 0.f;
+        qs[wave][2 * lane] = y0;
+        qs[wave][2 * lane + 1] = y1;
+    }
+    const bool completes = (pos + 1) % ratio == 0;
+    const uint32_t b_new = completes ? n_vis - 1 : 0xffffffffu;
+    if (completes && b_new >= rb && b_new < rb + SC_ROWS_WG && wave == 0) {
+        const float2 v = pool_block(raw2, pool, wn_k, ratio, b_new, n_rot, freq, eps, lane,
+                                    true, kh);
+        new_row[2 * lane] = v.x;
+        new_row[2 * lane + 1] = v.y;
+    }
+    __syncthreads();
+    const uint32_t g = lane & 7u;
+    float4 qr[4][4], nr[4];
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) qr[h][i] = *(const float4 *)&qs[h][32 * i + 4 * g];
+#pragma unroll
+    for (int i = 0; i < 4; i++) nr[i] = *(const float4 *)&new_row[32 * i + 4 * g];
+    score_rows(qr, pool, score, rb, n_vis, n_vis, lane, wave, nr[0], nr[1], nr[2], nr[3], b_new);
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -953,4 +1042,26 @@ extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t str
     qsa_topk_k<true><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0, width,
                                                    q4kv_pos_d);
     return q4kv_launch_ok("qsa_topk_d");
+}
+
+extern "C" bool q4_hip_qsa_index_score_d(void *raw_f16, float *pool, const float *wn_k,
+                                         const float *k_new, const float *q, const float *wn_q,
+                                         float *score, uint32_t stride, uint32_t n_head,
+                                         uint32_t hd, uint32_t ratio, uint32_t n_rot,
+                                         float rope_base, float eps) {
+    if (!q4kv_ok || !q4kv_pos_d || !raw_f16 || !pool || !k_new || !q || !score ||
+        hd != IDX_HD || n_head == 0 || n_head > 4 || ratio == 0 || n_rot > hd)
+        return false;
+    if (((uintptr_t)raw_f16 & 3u) || ((uintptr_t)pool & 15u) || ((uintptr_t)q & 15u) ||
+        ((uintptr_t)k_new & 7u) || ((uintptr_t)wn_k & 7u) || ((uintptr_t)wn_q & 7u)) {
+        Q4KV_ERR("qsa_index_score_d: misaligned buffer");
+        return false;
+    }
+    if (stride == 0) return true;
+    (void)hipGetLastError();
+    const uint32_t gx = (stride + SC_ROWS_WG - 1) / SC_ROWS_WG;
+    qsa_index_score_dk<<<gx, 256, 0, q4kv_stream>>>((uint32_t *)raw_f16, pool, wn_k, k_new, q,
+                                                    wn_q, score, n_head, ratio, n_rot,
+                                                    rope_base, eps, q4kv_pos_d);
+    return q4kv_launch_ok("qsa_index_score_d");
 }

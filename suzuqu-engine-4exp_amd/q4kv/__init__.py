@@ -104,6 +104,8 @@ SIGNATURES = {
     "q4_hip_qsa_score_d": (_b, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
     "q4_hip_qsa_topk": (_b, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
     "q4_hip_qsa_topk_d": (_b, [_vp, _vp, _u32, _u32, _u32, _u32]),
+    "q4_hip_qsa_index_score_d": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                      _u32, _f32, _f32]),
     "q4_hip_qsa_decode_n": (_b, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
                                  _u32, _f32, C.c_int]),
     "q4_hip_qsa_decode_idx": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,

@@ -322,3 +322,55 @@ def test_decode_indexer_chain(rt, oracle):
     assert np.array_equal(sel, want_sel)
     for p in (d_raw, d_wn, d_qw, d_pool, d_k, d_q, d_sc, d_sel):
         rt.free(p)
+
+
+@pytest.mark.parametrize("pos", [2, 3, 7, 1001, 262143])
+def test_fused_index_score_matches_separate_calls(rt, pos):
+    """q4_hip_qsa_index_score_d == f32_to_f16_d + pool_d + k_prep_d + score_d,
+    bit for bit (raw row, pool, scores), and q is left unmodified."""
+    lib = rt.lib
+    note(f"index_score_d pos={pos}")
+    rng = np.random.default_rng(pos + 5)
+    max_kv = 262144
+    max_blocks = max_kv // RATIO
+    n_pos = max(pos + 1, 64)
+    raw = raw_keys(rng, max_kv)
+    wn = (1 + 0.2 * rng.standard_normal(IDX_DIM)).astype(np.float32)
+    qw = (1 + 0.2 * rng.standard_normal(IDX_DIM)).astype(np.float32)
+    k = rng.standard_normal(IDX_DIM).astype(np.float32)
+    q = rng.standard_normal((IDX_HEADS, IDX_DIM)).astype(np.float32)
+    pool0 = (rng.standard_normal((max_blocks, IDX_DIM)) * 0.3).astype(np.float32)
+    outs = []
+    for fused in (False, True):
+        d_raw, d_pool, d_wn, d_qw = rt.upload(raw), rt.upload(pool0), rt.upload(wn), rt.upload(qw)
+        d_k, d_q = rt.upload(k), rt.upload(q)
+        d_sc = rt.upload(np.full(max_blocks, np.nan, np.float32))
+        d_sel = rt.alloc(WIDTH * 4)
+        lib.q4_hip_pos_push(pos)
+        if fused:
+            assert lib.q4_hip_qsa_index_score_d(d_raw, d_pool, d_wn, d_k, d_q, d_qw, d_sc,
+                                                max_blocks, IDX_HEADS, IDX_DIM, RATIO, N_ROT,
+                                                ROPE_BASE, RMS_EPS)
+        else:
+            assert lib.q4_hip_f32_to_f16_d(d_raw, IDX_DIM, d_k, IDX_DIM)
+            assert lib.q4_hip_qsa_pool_d(d_raw, d_pool, d_wn, IDX_DIM, RATIO, N_ROT, ROPE_BASE,
+                                         RMS_EPS)
+            assert lib.q4_hip_qsa_k_prep_d(d_q, d_qw, IDX_HEADS, IDX_DIM, N_ROT, ROPE_BASE,
+                                           RMS_EPS)
+            assert lib.q4_hip_qsa_score_d(d_q, d_pool, d_sc, max_blocks, IDX_HEADS, IDX_DIM,
+                                          RATIO)
+        assert lib.q4_hip_qsa_topk_d(d_sc, d_sel, max_blocks, K_BLK, RATIO, WIDTH)
+        rt.sync()
+        outs.append((rt.download(d_raw, raw.nbytes, np.uint16)[:n_pos * IDX_DIM],
+                     rt.download(d_pool, pool0.nbytes, np.float32),
+                     rt.download(d_sc, max_blocks * 4, np.float32),
+                     rt.download(d_sel, WIDTH * 4, np.int32),
+                     rt.download(d_q, q.nbytes, np.float32)))
+        for p in (d_raw, d_pool, d_wn, d_qw, d_k, d_q, d_sc, d_sel):
+            rt.free(p)
+    (r0, p0, s0, l0, _), (r1, p1, s1, l1, q1) = outs
+    assert np.array_equal(r0, r1)
+    assert np.array_equal(p0.view(np.uint32), p1.view(np.uint32))
+    assert np.array_equal(s0.view(np.uint32), s1.view(np.uint32))
+    assert np.array_equal(l0, l1)
+    assert np.array_equal(q1.reshape(q.shape), q)      # q untouched by the fused call
