@@ -519,6 +519,71 @@ def config4(b, steps=100, sets=4, layers=4):
 
 
 
+def config_prep(b, steps=200, sets=4, rot=64, base=1.0e7, eps=1.0e-6):
+    """Config 1's 12-layer decode step with the query/key preparation
+    (RMSNorm + RoPE of 16 query heads with their gates and of the 2 new key
+    rows) fused into the step kernel (q4_hip_qsa_step_prep_batch), against
+    the same step done as q_prep + k_prep per layer then the batched step."""
+    rt, lib = b.rt, b.lib
+    L = b.L
+    qg = rt.alloc(sets * L * N_HEAD * 2 * HD * 4)
+    b.gen(qg, sets * L * N_HEAD * 2 * HD, 91)
+    wq, wk = rt.alloc(HD * 4), rt.alloc(HD * 4)
+    b.gen(wq, HD, 92)
+    b.gen(wk, HD, 93)
+    gbuf = rt.alloc(L * N_HEAD * HD * 4)
+    qtmp = rt.alloc(L * N_HEAD * HD * 4)
+    ktmp = rt.alloc(sets * L * N_KVH * HD * 4)
+    preps = (q4kv.PrepStepDesc * (sets * L))()
+    steps_d = (q4kv.StepDesc * (sets * L))()
+    for r in range(sets):
+        for li in range(L):
+            i = r * L + li
+            qgp = qg + i * N_HEAD * 2 * HD * 4
+            out = b.d_out + li * QO_B
+            seq = q4kv.SeqDesc(b.kc[li], b.vc[li], qgp, gbuf + li * QO_B, out,
+                               b.sel_ptr(r, li), WIDTH, WIDTH, CTX, 0)
+            preps[i] = q4kv.PrepStepDesc(q4kv.StepDesc(seq, b.row_ptr(b.d_nk, r, li),
+                                                       b.row_ptr(b.d_nv, r, li), b.pos[r]),
+                                         wq, wk)
+            seq2 = q4kv.SeqDesc(b.kc[li], b.vc[li], qtmp + li * QO_B, gbuf + li * QO_B, out,
+                                b.sel_ptr(r, li), WIDTH, WIDTH, CTX, 0)
+            steps_d[i] = q4kv.StepDesc(seq2, ktmp + i * N_KVH * HD * 4,
+                                       b.row_ptr(b.d_nv, r, li), b.pos[r])
+    dp, ds = rt.alloc(C.sizeof(preps)), rt.alloc(C.sizeof(steps_d))
+    assert lib.q4_hip_h2d(dp, C.addressof(preps), C.sizeof(preps))
+    assert lib.q4_hip_h2d(ds, C.addressof(steps_d), C.sizeof(steps_d))
+    psz, ssz = C.sizeof(q4kv.PrepStepDesc), C.sizeof(q4kv.StepDesc)
+
+    def fused(r):
+        return lib.q4_hip_qsa_step_prep_batch(dp + r * L * psz, L, N_HEAD, N_KVH, HD, 1.0 / 16,
+                                              q4kv.KV_Q8, WIDTH, rot, base, eps)
+
+    def separate(r):
+        ok = True
+        for li in range(L):
+            i = r * L + li
+            ok &= lib.q4_hip_qsa_q_prep(qg + i * N_HEAD * 2 * HD * 4, wq, qtmp + li * QO_B,
+                                        gbuf + li * QO_B, N_HEAD, HD, rot, b.pos[r], base, eps)
+            ok &= lib.q4_hip_copy(ktmp + i * N_KVH * HD * 4, b.row_ptr(b.d_nk, r, li),
+                                  N_KVH * HD)
+            ok &= lib.q4_hip_qsa_k_prep(ktmp + i * N_KVH * HD * 4, wk, N_KVH, HD, rot,
+                                        b.pos[r], base, eps)
+        return ok and lib.q4_hip_qsa_step_batch(ds + r * L * ssz, L, N_HEAD, N_KVH, HD,
+                                                 1.0 / 16, q4kv.KV_Q8, WIDTH)
+
+    out = {"what": f"{L}-layer decode step with Q/K RMSNorm + RoPE (n_rot {rot}) of 16 query "
+                   "heads (+ gates) and the 2 new key rows",
+           "launches": {"fused": 2, "separate": 3 * L + 2}}
+    for name, fn in (("fused", fused), ("separate", separate)):
+        graphs = _graphs(lib, fn, sets)
+        t = _time_graphs(b, graphs, steps) / L
+        out[f"{name}_us_per_layer"] = round(t * 1e6, 3)
+    for p_ in (qg, wq, wk, gbuf, qtmp, ktmp, dp, ds):
+        rt.free(p_)
+    return out
+
+
 IDX_RATIO, IDX_KBLK, IDX_HEADS, IDX_DIM = 4, 512, 4, 128
 IDX_ROT, IDX_BASE, IDX_EPS = 64, 1.0e7, 1.0e-6
 
@@ -661,6 +726,7 @@ def main():
     if args.configs:
         configs = {"config2_batched_decode": config2(b), "config3_chunked_prefill": config3(b),
                    "config4_widths_restore": config4(b),
+                   "qk_prep_fused_step": config_prep(b),
                    "indexer_decode": config_indexer(b)}
     threads = min(16, os.cpu_count() or 1)
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)

@@ -180,6 +180,26 @@ bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32
                            uint32_t n_kvh, uint32_t hd, float scale, int kv_f16,
                            uint32_t max_n);
 
+/* A decode step with the query/key preparation fused in (src/q4_fwd.c:806-824:
+ * q4_hip_qsa_q_prep + q4_hip_qsa_k_prep + the append + the attention, in
+ * one launch plus the merge). step.seq.q points at the raw rows
+ * [n_head][q (hd) | gate (hd)]; step.seq.gate receives the gate halves
+ * ([n_head][hd], as q_prep's g) and gates the output (NULL: no gate);
+ * step.k is the raw K row (read, not modified). 128 bytes. */
+typedef struct {
+    q4kv_step_desc step;
+    const float *wn_q, *wn_k; /* RMSNorm weights [hd]; NULL = 1 */
+    uint64_t reserved[2];
+} q4kv_prep_step_desc;
+
+/* The same results as q4_hip_qsa_q_prep / q4_hip_qsa_k_prep (at step.pos,
+ * with n_rot, rope_base, eps) followed by q4_hip_qsa_step_batch, bit for bit.
+ * q8_0 caches with hd 256 and n_head / n_kvh <= 8 only. */
+bool q4_hip_qsa_step_prep_batch(const q4kv_prep_step_desc *d_descs, uint32_t n_seq,
+                                uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
+                                int kv_f16, uint32_t max_n, uint32_t n_rot, float rope_base,
+                                float eps);
+
 /* One token's K/V rows for one cache, for a batched append. */
 typedef struct {
     void *kcache, *vcache; /* cache bases (token 0) */

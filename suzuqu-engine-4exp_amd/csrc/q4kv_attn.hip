@@ -47,8 +47,11 @@ typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 
 /* MODE_STEP: MODE_BATCH over q4kv_step_desc entries, with the token's K/V
  * append done by the same launch (fast q8_0 kernel only). */
-enum { MODE_DENSE = 0, MODE_INDEXED = 1, MODE_BATCH = 2, MODE_STEP = 3 };
-#define IS_BATCH(M) ((M) == MODE_BATCH || (M) == MODE_STEP)
+/* MODE_PSTEP: MODE_STEP over q4kv_prep_step_desc entries, with the query
+ * and key preparation (RMSNorm + RoPE) done in the kernel. */
+enum { MODE_DENSE = 0, MODE_INDEXED = 1, MODE_BATCH = 2, MODE_STEP = 3, MODE_PSTEP = 4 };
+#define IS_STEP(M) ((M) == MODE_STEP || (M) == MODE_PSTEP)
+#define IS_BATCH(M) ((M) == MODE_BATCH || IS_STEP(M))
 
 struct AttnArgs {
     const uint8_t *kc, *vc;
@@ -63,6 +66,9 @@ struct AttnArgs {
     uint32_t n_head, n_kvh, hd;
     uint32_t S, cps, item0;
     float scale_log2;
+    /* MODE_PSTEP */
+    uint32_t n_rot;
+    float rope_base, eps;
 };
 
 struct Item {
@@ -78,6 +84,8 @@ struct Item {
     /* MODE_STEP: this KV head's new K/V rows and their position */
     const float *knew, *vnew;
     uint32_t pos_new;
+    /* MODE_PSTEP: RMSNorm weights; q rows are [q | gate] (head stride 2*hd) */
+    const float *wnq, *wnk;
 };
 
 template <int MODE>
@@ -87,6 +95,7 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
     const size_t hoff = (size_t)kh * gqa * a.hd;
     Item it;
     it.knew = it.vnew = nullptr;
+    it.wnq = it.wnk = nullptr;
     it.pos_new = ~0u;
     if (IS_BATCH(MODE)) {
         const q4kv_seq_desc *d =
@@ -96,7 +105,7 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
         const uint32_t n_sel = ldg(&d->n_sel);
         it.kc = (const uint8_t *)ldg(&d->kcache);
         it.vc = (const uint8_t *)ldg(&d->vcache);
-        it.q = ldg(&d->q) + hoff;
+        it.q = ldg(&d->q) + hoff * (MODE == MODE_PSTEP ? 2u : 1u);
         it.gate = gate ? gate + hoff : nullptr;
         it.out = ldg(&d->out) + hoff;
         it.max_kv = ldg(&d->max_kv);
@@ -104,11 +113,16 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
         it.n = idx ? n_sel : (n_sel < it.max_kv ? n_sel : it.max_kv);
         it.lsrc = idx ? it.list : (const int32_t *)a.seqs;
         it.lmask = idx ? ~0u : 0u;
-        if (MODE == MODE_STEP) {
+        if (IS_STEP(MODE)) {
             const q4kv_step_desc *sd = (const q4kv_step_desc *)d;
             it.knew = ldg(&sd->k) + (size_t)kh * a.hd;
             it.vnew = ldg(&sd->v) + (size_t)kh * a.hd;
             it.pos_new = ldg(&sd->pos);
+        }
+        if (MODE == MODE_PSTEP) {
+            const q4kv_prep_step_desc *pd = (const q4kv_prep_step_desc *)d;
+            it.wnq = ldg(&pd->wn_q);
+            it.wnk = ldg(&pd->wn_k);
         }
     } else {
         const size_t qo = (size_t)t * a.n_head * a.hd + hoff;
@@ -735,6 +749,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float qraw[8 * 260];
     __shared__ int32_t s_pos[CP];
     __shared__ float s_cmax[4][8], s_psum[4][8], s_ml[2][8];
+    __shared__ __attribute__((aligned(16))) float kst[MODE == MODE_PSTEP ? 256 : 1];
 
     TRACE(0);
     const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
@@ -761,11 +776,21 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
      * quantised rows to the caches, and any split whose chunk lists the
      * position uses the same bytes in LDS instead of the fetched row */
     float nx[4] = {0.f, 0.f, 0.f, 0.f};
-    const bool step_lane = MODE == MODE_STEP && tid < 128u;
+    const bool step_lane = IS_STEP(MODE) && tid < 128u;
     if (step_lane) {
         const float *src = (tid < 64u ? it.knew : it.vnew) + 32u * ((tid >> 3) & 7u) + 4u * (tid & 7u);
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) nx[i] = ldg(src + i);
+    }
+    if (MODE == MODE_PSTEP && wave == 0) {
+        /* wave 0 holds the K row (lane l: dims 4l .. 4l+3): RMSNorm + RoPE
+         * at the token's position, through LDS in the shared prep layout */
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) kst[4u * lane + i] = nx[i];
+        q4kv_prep_row(kst, kst, it.wnk, 256u, a.n_rot, (int32_t)it.pos_new, a.rope_base, a.eps,
+                      lane);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) nx[i] = kst[4u * lane + i];
     }
 
     /* rows this lane DMAs (u < 4 always valid, u = 4 only in wave 0) and the
@@ -782,14 +807,24 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     /* Q: one 1 KiB DMA per head row (coalesced), operands built after the
      * first chunk's barrier */
     const uint32_t g = mrow & 7u;
+    constexpr uint32_t QHS = MODE == MODE_PSTEP ? 512u : 256u; /* q head stride */
     if ((((uintptr_t)it.q) & 15u) == 0) {
         for (uint32_t h = wave; h < gqa; h += 4u)
-            dma16(it.q + (size_t)h * 256u + 4u * lane, qraw + h * 260u);
+            dma16(it.q + (size_t)h * QHS + 4u * lane, qraw + h * 260u);
     } else {
         for (uint32_t e = tid; e < gqa * 256u; e += 256u)
-            qraw[(e >> 8) * 260u + (e & 255u)] = ldg(it.q + e);
+            qraw[(e >> 8) * 260u + (e & 255u)] = ldg(it.q + (e >> 8) * QHS + (e & 255u));
     }
-    if (MODE == MODE_STEP && s == 0u && it.pos_new < it.max_kv && tid < 128u) {
+    if (MODE == MODE_PSTEP && s == 0u && it.gate) {
+        /* the gate halves of the [q | gate] rows go to the gate buffer the
+         * merge reads */
+        for (uint32_t e = tid; e < gqa * 64u; e += 256u) {
+            const uint32_t h = e >> 6, d = (e & 63u) * 4u;
+            *(float4 *)((float *)it.gate + (size_t)h * 256u + d) =
+                *(const float4 *)(it.q + (size_t)h * 512u + 256u + d);
+        }
+    }
+    if (IS_STEP(MODE) && s == 0u && it.pos_new < it.max_kv && tid < 128u) {
         int q[4];
         const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
         uint8_t *row = (uint8_t *)(tid < 64u ? kbase : vbase) + (size_t)it.pos_new * rstride;
@@ -836,7 +871,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         }
         TRACE(2);
         __builtin_amdgcn_s_waitcnt(0);
-        if (MODE == MODE_STEP) {
+        if (IS_STEP(MODE)) {
             /* rows at the appended position take the new token's bytes */
             const bool mine = tid < CP && pidx[NLD] >= 0 && (uint32_t)pidx[NLD] == it.pos_new;
             if (__syncthreads_or(mine)) {
@@ -854,6 +889,13 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         }
         TRACE(3);
         if (c == c0) {
+            if (MODE == MODE_PSTEP) {
+                /* query heads wave, wave + 4: RMSNorm + RoPE in place */
+                for (uint32_t h = wave; h < gqa; h += 4u)
+                    q4kv_prep_row(qraw + h * 260u, qraw + h * 260u, it.wnq, 256u, a.n_rot,
+                                  (int32_t)it.pos_new, a.rope_base, a.eps, lane);
+                __syncthreads();
+            }
             const float *qr = qraw + (g < gqa ? g : 0u) * 260u;
             const float qs = g < gqa ? 1.f : 0.f;
 #pragma unroll
@@ -1020,7 +1062,13 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 for (uint32_t j = 0; j < 4u; j++) {
                     const uint32_t d = d0 + j;
                     float rv = so[h * 256u + q8_col_of_dim(d)] * inv;
-                    if (it.gate) rv *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)h * 256u + d)));
+                    if (it.gate) {
+                        /* MODE_PSTEP: the gate half of the source row (the
+                         * copy above is for the merge kernel) */
+                        const float gv = MODE == MODE_PSTEP ? ldg(it.q + (size_t)h * 512u + 256u + d)
+                                                            : ldg(it.gate + (size_t)h * 256u + d);
+                        rv *= 1.f / (1.f + expf(-gv));
+                    }
                     o[j] = rv;
                 }
                 stg((f4_t *)(it.out + (size_t)h * 256u + d0), o);
@@ -1188,7 +1236,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
      * resident, the generic one about as many; more splits than that only
      * add a second round of workgroups and more partials to merge. */
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
-    if (MODE == MODE_STEP && !fast) return false; /* the fused append needs the fast kernel */
+    if (IS_STEP(MODE) && !fast) return false; /* the fused append needs the fast kernel */
     uint32_t S = (split_target() + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
@@ -1210,12 +1258,12 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
         if (fast)
             qsa_q8d256_k<MODE><<<grid, 256, 0, q4kv_stream>>>(a);
-        else if (MODE == MODE_STEP)
+        else if (IS_STEP(MODE))
             return false;
         else if (gqa <= 8u)
-            qsa_attn_k<KIND, MODE == MODE_STEP ? MODE_BATCH : MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
+            qsa_attn_k<KIND, IS_STEP(MODE) ? MODE_BATCH : MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
         else
-            qsa_attn_k<KIND, MODE == MODE_STEP ? MODE_BATCH : MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
+            qsa_attn_k<KIND, IS_STEP(MODE) ? MODE_BATCH : MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n++ + 1], q4kv_stream);
         if (S > 1u) qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
     }
@@ -1353,3 +1401,25 @@ extern "C" int q4kv_trace_read(uint64_t *host, size_t n) {
 #endif
 
 extern "C" bool q4_hip_qsa_topk_alloc(void) { return q4kv_ok && q4kv_part != nullptr; }
+
+extern "C" bool q4_hip_qsa_step_prep_batch(const q4kv_prep_step_desc *d_descs, uint32_t n_seq,
+                                           uint32_t n_head, uint32_t n_kvh, uint32_t hd,
+                                           float scale, int kv_f16, uint32_t max_n,
+                                           uint32_t n_rot, float rope_base, float eps) {
+    if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
+        return false;
+    const uint32_t gqa = n_head / n_kvh;
+    if (kv_f16 != Q4KV_Q8 || hd != 256u || gqa > 8u || n_rot > hd) {
+        Q4KV_ERR("qsa_step_prep_batch: needs a q8_0 cache, hd 256, gqa <= 8, n_rot <= hd");
+        return false;
+    }
+    (void)hipGetLastError();
+    AttnArgs a = base_args(nullptr, nullptr, nullptr, nullptr, nullptr, n_head, n_kvh, hd, 0,
+                           scale);
+    a.seqs = (const q4kv_seq_desc *)d_descs;
+    a.desc_stride = sizeof(q4kv_prep_step_desc);
+    a.n_rot = n_rot;
+    a.rope_base = rope_base;
+    a.eps = eps;
+    return launch_kind<Q4KV_Q8, MODE_PSTEP>(a, n_seq * n_kvh, max_n, gqa);
+}

@@ -49,41 +49,14 @@ constexpr uint32_t IDX_HD = 128;
 template <class T> __device__ inline T ld_vec(const T *p) { return *p; }
 template <class T> __device__ inline void st_vec(T *p, T v) { *p = v; }
 
-template <int CTRL> __device__ inline float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-/* Sum over the 8-lane group containing this lane, broadcast to all 8. */
-__device__ inline float sum8(float v) {
-    v += dpp<0xB1>(v);  /* quad_perm [1,0,3,2] */
-    v += dpp<0x4E>(v);  /* quad_perm [2,3,0,1] */
-    v += dpp<0x141>(v); /* row_half_mirror: lane i <-> 7-i */
-    return v;
-}
-__device__ inline float wave_sum(float v) {
-    v = sum8(v);
-    v += dpp<0x140>(v); /* row_mirror: the other half of the 16-lane row */
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
-}
-
-/* fp32 RoPE frequency base^(-(p/np)) with the exponent an fp32 quotient
- * (src/q4_rocm.cu:6255, 7391), correctly rounded: pow in double, rounded once.
- * At positions near 2^18 one ulp of freq moves the angle by ~0.016 rad, so the
- * frequency is not left to an approximate powf. */
+/* the shared wave arithmetic of q4kv_internal.h under short names */
+__device__ inline float sum8(float v) { return q4kv_sum8(v); }
+__device__ inline float wave_sum(float v) { return q4kv_wave_sum(v); }
 __device__ inline float rope_freq(float base, uint32_t p, uint32_t np) {
-    const float e = -__fdiv_rn((float)p, (float)np);
-    return (float)pow((double)base, (double)e);
+    return q4kv_rope_freq(base, p, np);
 }
-/* Rotate (x0, x1) by the fp32 angle pos * freq (one fp32 rounding, as the
- * reference forms it). */
 __device__ inline void rope_rotate(float &x0, float &x1, float pos_f, float freq) {
-    const float ang = __fmul_rn(pos_f, freq);
-    float s, c;
-    sincosf(ang, &s, &c);
-    const float a = x0, b = x1;
-    x0 = a * c - b * s;
-    x1 = a * s + b * c;
+    q4kv_rope_rotate(x0, x1, pos_f, freq);
 }
 
 /* --------------------------------------------------------------- pool ---- */
@@ -814,7 +787,6 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
 
 /* --------------------------------------------------------------- prep ---- */
 
-constexpr uint32_t PREP_MAXP = 8; /* pairs per lane: hd <= 1024 */
 
 /* RMSNorm * wn, then RoPE of pairs p < n_rot/2 at position pos, for one
  * (token, head) row per wave (src/q4_rocm.cu:6229-6289). GATE: the source
@@ -832,43 +804,18 @@ __global__ __launch_bounds__(256) void qsa_prep_k(const float *src, float *dst, 
     const uint32_t t = rowi / n_heads;
     const int32_t pos = (pp ? *pp : pos0) + (int32_t)t;
     const float *in = src + (size_t)rowi * hd * (GATE ? 2u : 1u);
-    float *o = dst + (size_t)rowi * hd;
-    const uint32_t np = hd / 2;
-    float2 x[PREP_MAXP];
-    float ss = 0.f;
-#pragma unroll
-    for (uint32_t m = 0; m < PREP_MAXP; m++) {
-        const uint32_t p = lane + 64u * m;
-        x[m] = p < np ? ld_vec((const float2 *)in + p) : make_float2(0.f, 0.f);
-        ss = fmaf(x[m].x, x[m].x, ss);
-        ss = fmaf(x[m].y, x[m].y, ss);
-    }
     if (GATE) {
         float *gd = g + (size_t)rowi * hd;
-#pragma unroll
-        for (uint32_t m = 0; m < PREP_MAXP; m++) {
-            const uint32_t p = lane + 64u * m;
-            if (p < np) st_vec((float2 *)gd + p, ld_vec((const float2 *)(in + hd) + p));
-        }
+        for (uint32_t p = lane; p < hd / 2; p += 64u)
+            st_vec((float2 *)gd + p, ld_vec((const float2 *)(in + hd) + p));
     }
-    ss = wave_sum(ss);
-    const float scale = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)hd) + eps));
-    const uint32_t nrp = n_rot / 2;
-#pragma unroll
-    for (uint32_t m = 0; m < PREP_MAXP; m++) {
-        const uint32_t p = lane + 64u * m;
-        if (p >= np) continue;
-        const float2 w = wn ? ld_vec((const float2 *)wn + p) : make_float2(1.f, 1.f);
-        float y0 = x[m].x * scale * w.x, y1 = x[m].y * scale * w.y;
-        if (p < nrp) rope_rotate(y0, y1, (float)pos, rope_freq(base, p, nrp));
-        st_vec((float2 *)o + p, make_float2(y0, y1));
-    }
+    q4kv_prep_row(in, dst + (size_t)rowi * hd, wn, hd, n_rot, pos, base, eps, lane);
 }
 
 bool prep_launch(const float *src, float *dst, float *g, const float *wn, uint32_t n_heads,
                  uint32_t hd, uint32_t n_rot, int32_t pos0, float base, float eps,
                  uint32_t n_tok, const int32_t *pp, const char *what) {
-    if (hd == 0 || (hd & 1u) || hd > 128u * PREP_MAXP || n_rot > hd) {
+    if (hd == 0 || (hd & 1u) || hd > 128u * Q4KV_PREP_MAXP || n_rot > hd) {
         Q4KV_ERR("%s: unsupported hd %u / n_rot %u", what, hd, n_rot);
         return false;
     }

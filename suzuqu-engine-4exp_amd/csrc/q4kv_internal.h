@@ -66,6 +66,76 @@ __device__ static inline void q8_lane_store(uint8_t *blk, uint32_t part, float d
     if (part == 0) *(uint16_t *)blk = __half_as_ushort(__float2half_rn(d));
 }
 
+/* ---- shared wave-level arithmetic of the Q/K preparation ---- */
+template <int CTRL> __device__ static inline float q4kv_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+/* Sum over the 8-lane group containing this lane, broadcast to all 8. */
+__device__ static inline float q4kv_sum8(float v) {
+    v += q4kv_dpp<0xB1>(v);  /* quad_perm [1,0,3,2] */
+    v += q4kv_dpp<0x4E>(v);  /* quad_perm [2,3,0,1] */
+    v += q4kv_dpp<0x141>(v); /* row_half_mirror: lane i <-> 7-i */
+    return v;
+}
+__device__ static inline float q4kv_wave_sum(float v) {
+    v = q4kv_sum8(v);
+    v += q4kv_dpp<0x140>(v); /* row_mirror: the other half of the 16-lane row */
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+/* fp32 RoPE frequency base^(-(p/np)) with the exponent an fp32 quotient
+ * (src/q4_rocm.cu:6255, 7391), correctly rounded: pow in double, rounded once.
+ * At positions near 2^18 one ulp of freq moves the angle by ~0.016 rad, so the
+ * frequency is not left to an approximate powf. */
+__device__ static inline float q4kv_rope_freq(float base, uint32_t p, uint32_t np) {
+    const float e = -__fdiv_rn((float)p, (float)np);
+    return (float)pow((double)base, (double)e);
+}
+/* Rotate (x0, x1) by the fp32 angle pos * freq (one fp32 rounding, as the
+ * reference forms it). */
+__device__ static inline void q4kv_rope_rotate(float &x0, float &x1, float pos_f, float freq) {
+    const float ang = __fmul_rn(pos_f, freq);
+    float s, c;
+    sincosf(ang, &s, &c);
+    const float a = x0, b = x1;
+    x0 = a * c - b * s;
+    x1 = a * s + b * c;
+}
+constexpr uint32_t Q4KV_PREP_MAXP = 8; /* pairs per lane: hd <= 1024 */
+/* One (token, head) row by one wave (src/q4_rocm.cu:6229-6289): RMSNorm
+ * times wn (NULL = 1), then RoPE of pairs p < n_rot/2 at position pos.
+ * Lane l owns pairs p = l + 64m; in and out may alias (every lane reads its
+ * pairs before the reduction). Every kernel that prepares rows calls this,
+ * so their results agree bit for bit. */
+__device__ static inline void q4kv_prep_row(const float *in, float *out, const float *wn,
+                                            uint32_t hd, uint32_t n_rot, int32_t pos,
+                                            float base, float eps, uint32_t lane) {
+    const uint32_t np = hd / 2;
+    float2 x[Q4KV_PREP_MAXP];
+    float ss = 0.f;
+#pragma unroll
+    for (uint32_t m = 0; m < Q4KV_PREP_MAXP; m++) {
+        const uint32_t p = lane + 64u * m;
+        x[m] = p < np ? make_float2(in[2 * p], in[2 * p + 1]) : make_float2(0.f, 0.f);
+        ss = fmaf(x[m].x, x[m].x, ss);
+        ss = fmaf(x[m].y, x[m].y, ss);
+    }
+    ss = q4kv_wave_sum(ss);
+    const float scale = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)hd) + eps));
+    const uint32_t nrp = n_rot / 2;
+#pragma unroll
+    for (uint32_t m = 0; m < Q4KV_PREP_MAXP; m++) {
+        const uint32_t p = lane + 64u * m;
+        if (p >= np) continue;
+        const float w0 = wn ? wn[2 * p] : 1.f, w1 = wn ? wn[2 * p + 1] : 1.f;
+        float y0 = x[m].x * scale * w0, y1 = x[m].y * scale * w1;
+        if (p < nrp) q4kv_rope_rotate(y0, y1, (float)pos, q4kv_rope_freq(base, p, nrp));
+        out[2 * p] = y0;
+        out[2 * p + 1] = y1;
+    }
+}
+
 #define Q4KV_ERR(...)                                                          \
     do {                                                                       \
         fprintf(stderr, "q4 hip: " __VA_ARGS__);                               \

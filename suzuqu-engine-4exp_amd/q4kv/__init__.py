@@ -47,6 +47,16 @@ class StepDesc(C.Structure):
 assert C.sizeof(StepDesc) == 96
 
 
+class PrepStepDesc(C.Structure):
+    """q4kv_prep_step_desc of include/q4kv.h (128 bytes)."""
+
+    _fields_ = [("step", StepDesc), ("wn_q", _vp), ("wn_k", _vp),
+                ("reserved", C.c_uint64 * 2)]
+
+
+assert C.sizeof(PrepStepDesc) == 128
+
+
 class AppendDesc(C.Structure):
     """q4kv_append_desc of include/q4kv.h (40 bytes)."""
 
@@ -104,6 +114,8 @@ SIGNATURES = {
     "q4_hip_qsa_score_d": (_b, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
     "q4_hip_qsa_topk": (_b, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
     "q4_hip_qsa_topk_d": (_b, [_vp, _vp, _u32, _u32, _u32, _u32]),
+    "q4_hip_qsa_step_prep_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32,
+                                        _u32, _f32, _f32]),
     "q4_hip_qsa_index_score_d": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                       _u32, _f32, _f32]),
     "q4_hip_qsa_decode_n": (_b, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
