@@ -511,10 +511,31 @@ def config4(b, steps=100, sets=4, layers=4):
         assert lib.q4kv_image_restore(C.byref(c), host, n_img, True)
     t = (time.perf_counter() - t0) / reps
     lib.q4_hip_host_free(host)
-    lib.q4kv_cache_close(C.byref(c))
     out["restore"] = {"what": "12 layers x 100000 tokens q8_0 K+V image, pinned host -> "
                               "device cache layout (host link bound)",
                       "bytes": nb, "ms": round(t * 1e3, 2), "gbs": round(nb / t / 1e9, 2)}
+    # the same image through a file (page cache), streamed through the pipe
+    path = os.path.join(os.environ.get("TMPDIR", "/tmp"), f"q4kv_bench_{os.getpid()}.img")
+    try:
+        c.n_kv = n_img
+        t0 = time.perf_counter()
+        ok = lib.q4kv_image_save_file(C.byref(c), path.encode())
+        t_save = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        n_back = lib.q4kv_image_restore_file(C.byref(c), path.encode())
+        t_file = time.perf_counter() - t0
+        if ok and n_back == n_img:
+            out["file_save"] = {"what": "device cache -> image file (D2H overlapped with the "
+                                        "writes, 32 MiB pinned chunks)", "bytes": nb,
+                                "ms": round(t_save * 1e3, 2), "gbs": round(nb / t_save / 1e9, 2)}
+            out["file_restore"] = {"what": "image file (page cache) -> device cache (reads "
+                                           "overlapped with the DMA)", "bytes": nb,
+                                   "ms": round(t_file * 1e3, 2),
+                                   "gbs": round(nb / t_file / 1e9, 2)}
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+    lib.q4kv_cache_close(C.byref(c))
     return out
 
 

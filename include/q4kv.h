@@ -228,6 +228,20 @@ bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc, ui
  * stream), or on the library's stream again when stream is NULL. */
 bool q4kv_use_stream(void *stream);
 
+/* Streamed file <-> device copies through pinned staging buffers of `chunk`
+ * bytes (the session image path; src/q4_fwd.c:2275-2294 stage synchronously
+ * through one pageable buffer). Reads of the next chunk overlap the DMA of
+ * the previous one, and device-to-host copies overlap the file writes. All
+ * copies are ordered on the library stream. q4kv_pipe_finish waits for every
+ * queued copy and write and reports whether all succeeded; after a failure
+ * the pipe refuses further work until finish. */
+typedef struct q4kv_pipe q4kv_pipe;
+q4kv_pipe *q4kv_pipe_open(size_t chunk);
+void q4kv_pipe_close(q4kv_pipe *p);
+bool q4kv_pipe_file_to_dev(q4kv_pipe *p, int fd, uint64_t off, void *dst, uint64_t n);
+bool q4kv_pipe_dev_to_file(q4kv_pipe *p, int fd, uint64_t off, const void *src, uint64_t n);
+bool q4kv_pipe_finish(q4kv_pipe *p);
+
 /* Pinned host buffers for restoring a session KV image (hipHostMalloc). */
 void *q4_hip_host_alloc(size_t n);
 void q4_hip_host_free(void *p);

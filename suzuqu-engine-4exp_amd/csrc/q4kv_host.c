@@ -12,6 +12,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <fcntl.h>
+#include <unistd.h>
 
 int q4kv_kind_of(const char *e) {
     if (!e) e = getenv("Q4_KV");
@@ -138,28 +140,35 @@ bool q4kv_image_save(const q4kv_cache *c, uint8_t *host_body) {
     return true;
 }
 
-/* Staged through a pinned buffer, one layer section at a time
- * (src/q4_fwd.c:2275-2294 stage through a pageable 16 MiB buffer). */
+/* Streamed through the pinned pipe: the device-to-host copy of the next
+ * chunk overlaps the file write of the previous one (src/q4_fwd.c:2275-2294
+ * stage through one pageable 16 MiB buffer, synchronously). The image is
+ * written to path.tmp and renamed into place only when complete. */
+#define Q4KV_IO_CHUNK ((size_t)32 << 20)
+
 bool q4kv_image_save_file(const q4kv_cache *c, const char *path) {
-    if (!c || !path) return false;
+    if (!c || !path || strlen(path) > 4096) return false;
     q4kv_img_hdr h = {Q4KV_IMG_MAGIC, Q4KV_IMG_VER, c->n_layer, c->n_kvh, c->hd,
                       c->max_kv,      c->n_kv,      q4kv_tag(c->kind)};
     char tmp[4096 + 8];
     snprintf(tmp, sizeof(tmp), "%s.tmp", path);
-    FILE *f = fopen(tmp, "wb");
-    if (!f) return false;
-    bool ok = fwrite(&h, sizeof(h), 1, f) == 1;
+    int fd = open(tmp, O_WRONLY | O_CREAT | O_TRUNC, 0644);
+    if (fd < 0) return false;
+    bool ok = pwrite(fd, &h, sizeof(h), 0) == (ssize_t)sizeof(h);
     const uint64_t sec = (uint64_t)c->n_kv * c->bpt;
-    uint8_t *stage = sec ? (uint8_t *)q4_hip_host_alloc(sec) : NULL;
-    if (sec && !stage) ok = false;
-    for (uint32_t l = 0; ok && sec && l < c->n_layer; l++) {
-        for (int is_v = 0; ok && is_v < 2; is_v++) {
-            ok = q4_hip_d2h(stage, q4kv_at(c, is_v, l, 0), sec) &&
-                 fwrite(stage, 1, sec, f) == sec;
+    if (ok && sec) {
+        q4kv_pipe *p = q4kv_pipe_open(Q4KV_IO_CHUNK);
+        uint64_t off = sizeof(h);
+        ok = p != NULL;
+        for (uint32_t l = 0; ok && l < c->n_layer; l++)
+            for (int is_v = 0; ok && is_v < 2; is_v++, off += sec)
+                ok = q4kv_pipe_dev_to_file(p, fd, off, q4kv_at(c, is_v, l, 0), sec);
+        if (p) {
+            ok = q4kv_pipe_finish(p) && ok;
+            q4kv_pipe_close(p);
         }
     }
-    q4_hip_host_free(stage);
-    if (fclose(f) != 0) ok = false;
+    if (close(fd) != 0) ok = false;
     if (!ok || rename(tmp, path) != 0) {
         remove(tmp);
         return false;
@@ -167,26 +176,31 @@ bool q4kv_image_save_file(const q4kv_cache *c, const char *path) {
     return true;
 }
 
+/* Streamed through the pinned pipe: the file read of the next chunk overlaps
+ * the DMA of the previous one (src/q4_fwd.c:2393-2470). */
 uint32_t q4kv_image_restore_file(q4kv_cache *c, const char *path) {
     if (!c || !c->d_k || !path) return 0;
-    FILE *f = fopen(path, "rb");
-    if (!f) return 0;
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) return 0;
     q4kv_img_hdr h;
-    bool ok = fread(&h, sizeof(h), 1, f) == 1 && h.magic == Q4KV_IMG_MAGIC &&
+    bool ok = pread(fd, &h, sizeof(h), 0) == (ssize_t)sizeof(h) && h.magic == Q4KV_IMG_MAGIC &&
               h.version == Q4KV_IMG_VER && h.n_layer == c->n_layer && h.n_kvh == c->n_kvh &&
               h.hd == c->hd && h.max_kv == c->max_kv && h.pad == q4kv_tag(c->kind) &&
               h.n_kv <= c->max_kv;
     const uint64_t sec = ok ? (uint64_t)h.n_kv * c->bpt : 0;
-    uint8_t *stage = sec ? (uint8_t *)q4_hip_host_alloc(sec) : NULL;
-    if (sec && !stage) ok = false;
-    for (uint32_t l = 0; ok && sec && l < c->n_layer; l++) {
-        for (int is_v = 0; ok && is_v < 2; is_v++) {
-            ok = fread(stage, 1, sec, f) == sec &&
-                 q4_hip_h2d(q4kv_at(c, is_v, l, 0), stage, sec);
+    if (ok && sec) {
+        q4kv_pipe *p = q4kv_pipe_open(Q4KV_IO_CHUNK);
+        uint64_t off = sizeof(h);
+        ok = p != NULL;
+        for (uint32_t l = 0; ok && l < c->n_layer; l++)
+            for (int is_v = 0; ok && is_v < 2; is_v++, off += sec)
+                ok = q4kv_pipe_file_to_dev(p, fd, off, q4kv_at(c, is_v, l, 0), sec);
+        if (p) {
+            ok = q4kv_pipe_finish(p) && ok;
+            q4kv_pipe_close(p);
         }
     }
-    q4_hip_host_free(stage);
-    fclose(f);
+    close(fd);
     if (!ok) {
         c->n_kv = 0;
         return 0;

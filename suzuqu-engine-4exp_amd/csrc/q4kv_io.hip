@@ -1,0 +1,151 @@
+/*
+ * q4kv_io.hip -- streamed session-image I/O between a file and device memory.
+ *
+ * The reference stages the K/V image sections through one pageable 16 MiB
+ * buffer, synchronously: read, copy, read, copy (src/q4_fwd.c:2275-2294,
+ * 2393-2470). Here a pipe of Q4KV_PIPE_NBUF pinned buffers moves the bytes
+ * on the library stream with one event per buffer, so the file read of
+ * chunk i+1 overlaps the DMA of chunk i (restore), and the device-to-host
+ * copy of chunk i+1 overlaps the file write of chunk i (save). Pinned
+ * buffers are allocated (hipHostMalloc), never registered.
+ */
+#include <hip/hip_runtime.h>
+#include <errno.h>
+#include <stdlib.h>
+#include <unistd.h>
+
+#include "q4kv_internal.h"
+
+extern "C" {
+#include "q4kv.h"
+}
+
+#define Q4KV_PIPE_NBUF 3
+
+struct q4kv_pipe {
+    uint8_t *buf[Q4KV_PIPE_NBUF];
+    hipEvent_t ev[Q4KV_PIPE_NBUF];
+    /* save: the file range each in-flight buffer still has to be written to */
+    int fd[Q4KV_PIPE_NBUF];
+    uint64_t off[Q4KV_PIPE_NBUF], len[Q4KV_PIPE_NBUF];
+    bool busy[Q4KV_PIPE_NBUF];
+    size_t chunk;
+    unsigned next;
+    bool failed;
+};
+
+static bool read_full(int fd, uint8_t *p, uint64_t n, uint64_t off) {
+    while (n) {
+        const ssize_t r = pread(fd, p, n, (off_t)off);
+        if (r < 0 && errno == EINTR) continue;
+        if (r <= 0) return false;
+        p += r;
+        off += (uint64_t)r;
+        n -= (uint64_t)r;
+    }
+    return true;
+}
+
+static bool write_full(int fd, const uint8_t *p, uint64_t n, uint64_t off) {
+    while (n) {
+        const ssize_t r = pwrite(fd, p, n, (off_t)off);
+        if (r < 0 && errno == EINTR) continue;
+        if (r <= 0) return false;
+        p += r;
+        off += (uint64_t)r;
+        n -= (uint64_t)r;
+    }
+    return true;
+}
+
+/* Wait for buffer i's copy; for a pending save, write its bytes out. */
+static bool retire(q4kv_pipe *p, unsigned i) {
+    if (!p->busy[i]) return true;
+    p->busy[i] = false;
+    if (hipEventSynchronize(p->ev[i]) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (p->fd[i] >= 0 && !write_full(p->fd[i], p->buf[i], p->len[i], p->off[i])) return false;
+    return true;
+}
+
+extern "C" q4kv_pipe *q4kv_pipe_open(size_t chunk) {
+    if (!q4kv_ok || chunk == 0) return nullptr;
+    q4kv_pipe *p = (q4kv_pipe *)calloc(1, sizeof(q4kv_pipe));
+    if (!p) return nullptr;
+    p->chunk = chunk;
+    for (int i = 0; i < Q4KV_PIPE_NBUF; i++) {
+        p->fd[i] = -1;
+        if (hipHostMalloc((void **)&p->buf[i], chunk, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&p->ev[i], hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            q4kv_pipe_close(p);
+            return nullptr;
+        }
+    }
+    return p;
+}
+
+extern "C" bool q4kv_pipe_finish(q4kv_pipe *p) {
+    if (!p) return false;
+    bool ok = !p->failed;
+    for (unsigned k = 0; k < Q4KV_PIPE_NBUF; k++)
+        ok = retire(p, (p->next + k) % Q4KV_PIPE_NBUF) && ok; /* oldest first */
+    p->failed = false;
+    return ok;
+}
+
+extern "C" void q4kv_pipe_close(q4kv_pipe *p) {
+    if (!p) return;
+    (void)q4kv_pipe_finish(p);
+    for (int i = 0; i < Q4KV_PIPE_NBUF; i++) {
+        if (p->buf[i]) (void)hipHostFree(p->buf[i]);
+        if (p->ev[i]) (void)hipEventDestroy(p->ev[i]);
+    }
+    free(p);
+}
+
+extern "C" bool q4kv_pipe_file_to_dev(q4kv_pipe *p, int fd, uint64_t off, void *dst,
+                                      uint64_t n) {
+    if (!p || fd < 0 || !dst || p->failed) return false;
+    uint8_t *d = (uint8_t *)dst;
+    for (uint64_t o = 0; o < n; o += p->chunk) {
+        const uint64_t len = n - o < p->chunk ? n - o : p->chunk;
+        const unsigned i = p->next++ % Q4KV_PIPE_NBUF;
+        if (!retire(p, i) || !read_full(fd, p->buf[i], len, off + o) ||
+            hipMemcpyAsync(d + o, p->buf[i], len, hipMemcpyHostToDevice, q4kv_stream) !=
+                hipSuccess ||
+            hipEventRecord(p->ev[i], q4kv_stream) != hipSuccess) {
+            (void)hipGetLastError();
+            p->failed = true;
+            return false;
+        }
+        p->fd[i] = -1;
+        p->busy[i] = true;
+    }
+    return true;
+}
+
+extern "C" bool q4kv_pipe_dev_to_file(q4kv_pipe *p, int fd, uint64_t off, const void *src,
+                                      uint64_t n) {
+    if (!p || fd < 0 || !src || p->failed) return false;
+    const uint8_t *s = (const uint8_t *)src;
+    for (uint64_t o = 0; o < n; o += p->chunk) {
+        const uint64_t len = n - o < p->chunk ? n - o : p->chunk;
+        const unsigned i = p->next++ % Q4KV_PIPE_NBUF;
+        if (!retire(p, i) ||
+            hipMemcpyAsync(p->buf[i], s + o, len, hipMemcpyDeviceToHost, q4kv_stream) !=
+                hipSuccess ||
+            hipEventRecord(p->ev[i], q4kv_stream) != hipSuccess) {
+            (void)hipGetLastError();
+            p->failed = true;
+            return false;
+        }
+        p->fd[i] = fd;
+        p->off[i] = off + o;
+        p->len[i] = len;
+        p->busy[i] = true;
+    }
+    return true;
+}

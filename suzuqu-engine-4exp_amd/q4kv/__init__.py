@@ -116,6 +116,11 @@ SIGNATURES = {
     "q4_hip_qsa_topk_d": (_b, [_vp, _vp, _u32, _u32, _u32, _u32]),
     "q4_hip_qsa_step_prep_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32,
                                         _u32, _f32, _f32]),
+    "q4kv_pipe_open": (_vp, [C.c_size_t]),
+    "q4kv_pipe_close": (None, [_vp]),
+    "q4kv_pipe_file_to_dev": (_b, [_vp, C.c_int, _u64, _vp, _u64]),
+    "q4kv_pipe_dev_to_file": (_b, [_vp, C.c_int, _u64, _vp, _u64]),
+    "q4kv_pipe_finish": (_b, [_vp]),
     "q4_hip_qsa_index_score_d": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                       _u32, _f32, _f32]),
     "q4_hip_qsa_decode_n": (_b, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,

@@ -101,6 +101,79 @@ def test_image_file_roundtrip_and_guard(rt, tmp_path):
             rt.lib.q4kv_cache_close(C.byref(x))
 
 
+def test_pipe_streams_odd_chunks_both_ways(rt, tmp_path):
+    """The staged file <-> device pipe with a chunk much smaller than the
+    sections (many buffer reuses), odd sizes and offsets; a short file fails
+    the read and the pipe reports it at finish."""
+    note("pipe file <-> device")
+    lib = rt.lib
+    rng = np.random.default_rng(720)
+    sizes = [1, 999, 1000, 1001, 7777, 65536 + 3]
+    blobs = [rng.integers(0, 256, n, dtype=np.uint8) for n in sizes]
+    path = tmp_path / "pipe.bin"
+    hdr = 13
+    with open(path, "wb") as f:
+        f.write(b"x" * hdr)
+        for b in blobs:
+            f.write(b.tobytes())
+    dst = [rt.alloc(n) for n in sizes]
+    p = lib.q4kv_pipe_open(1000)
+    assert p
+    fd = os.open(path, os.O_RDONLY)
+    off = hdr
+    for d, n in zip(dst, sizes):
+        assert lib.q4kv_pipe_file_to_dev(p, fd, off, d, n)
+        off += n
+    assert lib.q4kv_pipe_finish(p)
+    os.close(fd)
+    for d, b in zip(dst, blobs):
+        assert np.array_equal(rt.download(d, b.size, np.uint8), b)
+    # device -> file at other offsets, read back on the host
+    out = tmp_path / "out.bin"
+    fd = os.open(out, os.O_WRONLY | os.O_CREAT | os.O_TRUNC, 0o644)
+    off = 5
+    for d, n in zip(dst, sizes):
+        assert lib.q4kv_pipe_dev_to_file(p, fd, off, d, n)
+        off += n
+    assert lib.q4kv_pipe_finish(p)
+    os.close(fd)
+    data = np.fromfile(out, np.uint8)
+    assert np.array_equal(data[5:], np.concatenate(blobs))
+    # a read past the end of the file fails, and finish reports it
+    fd = os.open(path, os.O_RDONLY)
+    ok = lib.q4kv_pipe_file_to_dev(p, fd, os.path.getsize(path) - 10, dst[-1], sizes[-1])
+    assert not ok
+    assert not lib.q4kv_pipe_finish(p)           # reports the failure once
+    assert lib.q4kv_pipe_finish(p)               # then the pipe is usable again
+    os.close(fd)
+    lib.q4kv_pipe_close(p)
+    for d in dst:
+        rt.free(d)
+
+
+def test_image_file_truncated_body_is_refused(rt, tmp_path):
+    note("session image file, truncated")
+    rng = np.random.default_rng(711)
+    c = _open(rt, 2, 2, 512)
+    d = _open(rt, 2, 2, 512)
+    try:
+        n = 400
+        for layer in range(2):
+            for is_v in (0, 1):
+                rt.h2d(rt.lib.q4kv_at(C.byref(c), is_v, layer, 0),
+                       rng.integers(0, 256, n * c.bpt, dtype=np.uint8))
+        c.n_kv = n
+        path = str(tmp_path / "img.q4kv")
+        assert rt.lib.q4kv_image_save_file(C.byref(c), path.encode())
+        with open(path, "r+b") as f:
+            f.truncate(os.path.getsize(path) - 1)
+        d.n_kv = 7
+        assert rt.lib.q4kv_image_restore_file(C.byref(d), path.encode()) == 0 and d.n_kv == 0
+    finally:
+        for x in (c, d):
+            rt.lib.q4kv_cache_close(C.byref(x))
+
+
 def test_config4_restore_100k_image_then_decode(rt, oracle):
     """Config 4: restore a 100000-token q8_0 image of 12 QSA layers from pinned
     host memory into the device layout, then decode 256 tokens (append +
