@@ -605,6 +605,63 @@ def config_prep(b, steps=200, sets=4, rot=64, base=1.0e7, eps=1.0e-6):
     return out
 
 
+def config_out(b, steps=100, sets=4, n_embd=4096):
+    """Config 1's 12-layer decode step followed by each layer's q8_0
+    attention output projection (W_o [n_embd][16 x 256], synthetic weights):
+    the merge epilogue fused with the GEMV (q4_hip_qsa_step_out_batch)
+    against the batched step then one q4_hip_gemv_dd per layer."""
+    rt, lib = b.rt, b.lib
+    L = b.L
+    ncols = N_HEAD * HD
+    wbytes = n_embd * ncols // 32 * 34
+    tmp = rt.alloc(n_embd * ncols * 4)
+    ws = []
+    for li in range(L):
+        wq = rt.alloc(wbytes)
+        b.gen(tmp, n_embd * ncols, 300 + li)
+        assert lib.q4_hip_f32_to_q8(wq, tmp, n_embd * ncols)
+        ws.append(wq)
+    rt.sync()
+    rt.free(tmp)
+    ys = rt.alloc(L * n_embd * 4)
+    outs = (q4kv.OutDesc * L)()
+    for li in range(L):
+        outs[li] = q4kv.OutDesc(ws[li], ys + li * n_embd * 4)
+    dd = rt.alloc(C.sizeof(outs))
+    assert lib.q4_hip_h2d(dd, C.addressof(outs), C.sizeof(outs))
+    ssz = C.sizeof(q4kv.StepDesc)
+
+    def fused(r):
+        return lib.q4_hip_qsa_step_out_batch(b.d_step + r * L * ssz, dd, L, N_HEAD, N_KVH, HD,
+                                             1.0 / 16, q4kv.KV_Q8, WIDTH, n_embd, 1.0)
+
+    def separate(r):
+        ok = b._enqueue_batched(r)
+        for li in range(L):
+            ok &= lib.q4_hip_gemv_dd(8, ws[li], n_embd, ncols, b.d_out + li * QO_B,
+                                     ys + li * n_embd * 4, 1.0)
+        return ok
+
+    out = {"what": f"{L}-layer decode step + attn_output projection per layer (q8_0 "
+                   f"[{n_embd}][{ncols}], {wbytes} B per layer)",
+           "launches": {"fused": 2, "separate": 2 + L}}
+    for name, fn in (("fused", fused), ("separate", separate)):
+        graphs = _graphs(lib, fn, min(sets, b.R))
+        t = _time_graphs(b, graphs, steps) / L
+        out[f"{name}_us_per_layer"] = round(t * 1e6, 3)
+    # the GEMV alone: one launch per layer, W streamed from HBM (12 x 17.8 MB)
+    graphs = _graphs(lib, lambda r: all(lib.q4_hip_gemv_dd(8, ws[li], n_embd, ncols,
+                                                           b.d_out + li * QO_B,
+                                                           ys + li * n_embd * 4, 1.0)
+                                        for li in range(L)), 1)
+    t = _time_graphs(b, graphs, steps) / L
+    out["gemv_us_per_layer"] = round(t * 1e6, 3)
+    out["gemv_gbs"] = round((wbytes + ncols * 4 + n_embd * 4) / t / 1e9, 1)
+    for p_ in ws + [ys, dd]:
+        rt.free(p_)
+    return out
+
+
 IDX_RATIO, IDX_KBLK, IDX_HEADS, IDX_DIM = 4, 512, 4, 128
 IDX_ROT, IDX_BASE, IDX_EPS = 64, 1.0e7, 1.0e-6
 
@@ -748,6 +805,7 @@ def main():
         configs = {"config2_batched_decode": config2(b), "config3_chunked_prefill": config3(b),
                    "config4_widths_restore": config4(b),
                    "qk_prep_fused_step": config_prep(b),
+                   "out_projection_fused": config_out(b),
                    "indexer_decode": config_indexer(b)}
     threads = min(16, os.cpu_count() or 1)
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)

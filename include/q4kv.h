@@ -127,6 +127,12 @@ bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok, uint32_t 
 bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride, uint32_t k_blk,
                        uint32_t ratio, uint32_t width);                 /* src/q4.h:705-706 */
 
+/* ---------------- attention output projection ----------------
+ * y[r] = scale * sum_c W[r][c] x[c] with W in q8_0 rows (ncols/32 blocks of
+ * 34 bytes). Only ggml type 8 (q8_0) is supported; other types return false. */
+bool q4_hip_gemv_dd(uint32_t ggml_type, const uint8_t *d_w, uint64_t nrows, uint64_t ncols,
+                    const float *d_x, float *d_y, float scale);         /* src/q4.h:720-721 */
+
 /* ---------------- extensions (no reference counterpart) ----------------
  * Additive entry points; nothing above depends on them. */
 
@@ -199,6 +205,24 @@ bool q4_hip_qsa_step_prep_batch(const q4kv_prep_step_desc *d_descs, uint32_t n_s
                                 uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
                                 int kv_f16, uint32_t max_n, uint32_t n_rot, float rope_base,
                                 float eps);
+
+/* The attention output projection of one item, for q4_hip_qsa_step_out_batch. */
+typedef struct {
+    const uint8_t *w_o; /* q8_0 attn_output weight [n_embd][n_head*hd / 32 blocks] */
+    float *y;           /* [n_embd]: y += y_scale * w_o . out */
+} q4kv_out_desc;
+
+/* q4_hip_qsa_step_batch with the merge epilogue fused into the attention
+ * output projection (src/q4_fwd.c:922-927: the gated merge, then the q8_0
+ * attn_output GEMV): each item's merged, gated output is written to its
+ * seq.out and y += y_scale * w_o . out is accumulated with fp32 atomics (the
+ * heads' contributions to a row are summed in arrival order, so y matches
+ * q4_hip_gemv_dd + add within rounding, not bit for bit). Two launches per
+ * call. q8_0 caches with hd 256 and n_head / n_kvh <= 8 only. */
+bool q4_hip_qsa_step_out_batch(const q4kv_step_desc *d_descs, const q4kv_out_desc *d_outs,
+                               uint32_t n_seq, uint32_t n_head, uint32_t n_kvh, uint32_t hd,
+                               float scale, int kv_f16, uint32_t max_n, uint32_t n_embd,
+                               float y_scale);
 
 /* One token's K/V rows for one cache, for a batched append. */
 typedef struct {

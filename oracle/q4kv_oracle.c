@@ -301,3 +301,26 @@ int orc_attn(const float *q, const void *kcache, const void *vcache, int kind,
     }
     return err;
 }
+
+/* q8_0 GEMV: y[r] = scale * sum_b d_b * sum_i q_bi * x[32b + i] over the
+ * ncols/32 blocks of row r (34 bytes each: fp16 d, 32 int8), accumulated in
+ * double. src/q4_rocm.cu:1262-1285 (wgv_q8_0_k), q8_0 layout
+ * src/q4_quant.c:123-133. */
+int orc_gemv_q8_0(const uint8_t *w, uint64_t nrows, uint64_t ncols, const float *x, float *y,
+                  float scale) {
+    if (!w || !x || !y || ncols % 32) return -1;
+    const uint64_t nb = ncols / 32;
+    for (uint64_t r = 0; r < nrows; r++) {
+        const uint8_t *row = w + r * nb * 34;
+        double acc = 0;
+        for (uint64_t b = 0; b < nb; b++) {
+            const uint8_t *blk = row + b * 34;
+            const double d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+            double s = 0;
+            for (int i = 0; i < 32; i++) s += (double)(int8_t)blk[2 + i] * x[b * 32 + i];
+            acc += d * s;
+        }
+        y[r] = (float)(acc * scale);
+    }
+    return 0;
+}

@@ -36,6 +36,9 @@
  *                      formed from orc_rope_freq, which is checked against
  *                      numpy float32 arithmetic.
  *   orc_qsa_score      numpy float64 einsum + relu + -1e30 mask.
+ *   orc_gemv_q8_0      the reference's own q4_dequant_row (oracle/_ref) times x
+ *                      in float64 (an independent dequantisation), and closed
+ *                      forms: identity-like weights pick one column of x.
  */
 #ifndef Q4KV_ORACLE_H
 #define Q4KV_ORACLE_H
@@ -85,6 +88,10 @@ int orc_attn(const float *q, const void *kcache, const void *vcache, int kind,
              uint32_t hd, uint32_t n_tok, const int32_t *idx, uint32_t width,
              uint64_t tok_stride, uint64_t kvh_stride, uint32_t kv_base,
              uint32_t max_kv, float scale, int dbl, int nthreads);
+
+/* q8_0 GEMV y = scale * W x, W [nrows][ncols/32 blocks] (src/q4_rocm.cu:1262-1285). */
+int orc_gemv_q8_0(const uint8_t *w, uint64_t nrows, uint64_t ncols, const float *x, float *y,
+                  float scale);
 
 /* ---- QSA indexer and Q/K preparation (oracle/qsa_index_oracle.c) ---- */
 /* Order-preserving key of an fp32 score, src/q4_rocm.cu:7471-7474. */

@@ -1173,6 +1173,85 @@ __global__ __launch_bounds__(256) void qsa_comb_k(AttnArgs a) {
     stg(it.out + (size_t)g * hd + dim, r);
 }
 
+/* The merge epilogue fused with the attention output projection
+ * (src/q4_fwd.c:922-927: the split merge with its gate, then the q8_0
+ * attn_output GEMV): workgroup (head, row block) of item seq merges that
+ * head's split partials exactly as qsa_comb_k does (or, with one split,
+ * reads the finished output), keeps the gated head row in LDS, writes it to
+ * the output buffer (row block 0), and adds y_scale * W[rows][head cols] x_h
+ * into y with fp32 atomics: four lanes per row, two q8_0 blocks each. The
+ * sixteen heads' contributions to a row are summed in arrival order. */
+constexpr uint32_t OUT_RPB = 256; /* W rows per workgroup */
+
+template <int MODE>
+__global__ __launch_bounds__(256) void qsa_comb_gemv_k(AttnArgs a, const q4kv_out_desc *od,
+                                                       uint32_t n_embd, uint32_t n_rb,
+                                                       float y_scale) {
+    __shared__ __attribute__((aligned(16))) float xh[256];
+    __shared__ float xsum[8];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t h = blockIdx.x / n_rb, rb = blockIdx.x - h * n_rb, seq = blockIdx.y;
+    const uint32_t gqa = a.n_head / a.n_kvh, hd = a.hd, S = a.S;
+    const uint32_t kh = h / gqa, g = h - kh * gqa, item = seq * a.n_kvh + kh;
+    const uint32_t dim = col_dim<Q4KV_Q8>(tid);
+    const Item it = resolve_item<MODE>(a, item);
+    float r;
+    if (S > 1u) {
+        const float *pb = a.part + ((size_t)item * S * gqa + g) * PSTRIDE;
+        const size_t sst = (size_t)gqa * PSTRIDE;
+        float L = 0.f, acc;
+        if (S <= 8u) acc = comb_reg<8>(pb, sst, S, tid, L);
+        else if (S <= 16u) acc = comb_reg<16>(pb, sst, S, tid, L);
+        else if (S <= 24u) acc = comb_reg<24>(pb, sst, S, tid, L);
+        else if (S <= 32u) acc = comb_reg<32>(pb, sst, S, tid, L);
+        else if (S <= 48u) acc = comb_reg<48>(pb, sst, S, tid, L);
+        else if (S <= COMB_REG) acc = comb_reg<COMB_REG>(pb, sst, S, tid, L);
+        else {
+            float M = -INFINITY;
+            acc = 0.f;
+            for (uint32_t sp = 0; sp < S; sp++)
+                if (ldg(pb + sp * sst + 1u) > 0.f) M = fmax2(M, ldg(pb + sp * sst));
+            for (uint32_t sp = 0; sp < S; sp++) {
+                const float l = ldg(pb + sp * sst + 1u);
+                if (l > 0.f) {
+                    const float w = __builtin_amdgcn_exp2f(ldg(pb + sp * sst) - M);
+                    L += w * l;
+                    acc += w * ldg(pb + sp * sst + 2u + tid);
+                }
+            }
+        }
+        r = L > 0.f ? acc / L : 0.f;
+        if (it.gate) r *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)g * hd + dim)));
+        if (rb == 0) stg(it.out + (size_t)g * hd + dim, r);
+    } else {
+        r = ldg(it.out + (size_t)g * hd + dim); /* one split: already merged and gated */
+    }
+    xh[dim] = r;
+    __syncthreads();
+    if (tid < 8u) {
+        float sx = 0.f;
+        for (int i = 0; i < 32; i++) sx += xh[32u * tid + i];
+        xsum[tid] = sx;
+    }
+    __syncthreads();
+    const uint8_t *w = (const uint8_t *)ldg(&od[seq].w_o);
+    float *y = ldg(&od[seq].y);
+    const size_t rowb = (size_t)(a.n_head * hd / 32u) * 34u;
+    const uint32_t pr = lane & 3u; /* this lane's block pair (64 columns) */
+    const uint32_t rend = min(n_embd, (rb + 1u) * OUT_RPB);
+    const float xa = xsum[2u * pr], xb = xsum[2u * pr + 1u];
+    for (uint32_t row = rb * OUT_RPB + wave * 16u + (lane >> 2); row < rend; row += 64u) {
+        uint32_t dw[17];
+        const uint32_t *src = (const uint32_t *)(w + (size_t)row * rowb + (size_t)h * 272u + 68u * pr);
+#pragma unroll
+        for (int k = 0; k < 17; k++) dw[k] = ldg(src + k);
+        float part = q4kv_q8_pair_dot(dw, xh, pr, xa, xb);
+        part += q4kv_dpp<0xB1>(part); /* the row's four lanes */
+        part += q4kv_dpp<0x4E>(part);
+        if (pr == 0) atomicAdd(y + row, y_scale * part);
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 
 /* Live timing of the split-KV kernel: HIP events recorded on the library
@@ -1228,8 +1307,15 @@ static uint32_t split_target(void) {
 }
 #define Q4KV_MAX_GRID_Y 65535u
 
+struct OutProj {
+    const q4kv_out_desc *od;
+    uint32_t n_embd;
+    float y_scale;
+};
+
 template <int KIND, int MODE>
-static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa) {
+static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa,
+                        const OutProj *op = nullptr) {
     constexpr uint32_t CP = KCfg<KIND>::CP;
     const uint32_t n_chunks = (max_n + CP - 1u) / CP;
     /* Fill the chip once: the fast q8 kernel keeps 2 workgroups per CU
@@ -1265,7 +1351,14 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         else
             qsa_attn_k<KIND, IS_STEP(MODE) ? MODE_BATCH : MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n++ + 1], q4kv_stream);
-        if (S > 1u) qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
+        if (S > 1u && !op) qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
+    }
+    if (op) {
+        if (!fast) return false;
+        a.item0 = 0;
+        const uint32_t n_rb = (op->n_embd + OUT_RPB - 1u) / OUT_RPB;
+        qsa_comb_gemv_k<MODE><<<dim3(a.n_head * n_rb, n_items / a.n_kvh), 256, 0, q4kv_stream>>>(
+            a, op->od, op->n_embd, n_rb, op->y_scale);
     }
     return q4kv_launch_ok("qsa attention");
 }
@@ -1422,4 +1515,26 @@ extern "C" bool q4_hip_qsa_step_prep_batch(const q4kv_prep_step_desc *d_descs, u
     a.rope_base = rope_base;
     a.eps = eps;
     return launch_kind<Q4KV_Q8, MODE_PSTEP>(a, n_seq * n_kvh, max_n, gqa);
+}
+
+extern "C" bool q4_hip_qsa_step_out_batch(const q4kv_step_desc *d_descs,
+                                          const q4kv_out_desc *d_outs, uint32_t n_seq,
+                                          uint32_t n_head, uint32_t n_kvh, uint32_t hd,
+                                          float scale, int kv_f16, uint32_t max_n,
+                                          uint32_t n_embd, float y_scale) {
+    if (!q4kv_ok || !d_descs || !d_outs || !n_seq || !max_n || !n_embd ||
+        !shape_ok(n_head, n_kvh, hd, kv_f16))
+        return false;
+    const uint32_t gqa = n_head / n_kvh;
+    if (kv_f16 != Q4KV_Q8 || hd != 256u || gqa > 8u || n_seq > 65535u) {
+        Q4KV_ERR("qsa_step_out_batch: needs a q8_0 cache, hd 256, gqa <= 8");
+        return false;
+    }
+    (void)hipGetLastError();
+    AttnArgs a = base_args(nullptr, nullptr, nullptr, nullptr, nullptr, n_head, n_kvh, hd, 0,
+                           scale);
+    a.seqs = (const q4kv_seq_desc *)d_descs;
+    a.desc_stride = sizeof(q4kv_step_desc);
+    const OutProj op = {d_outs, n_embd, y_scale};
+    return launch_kind<Q4KV_Q8, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, &op);
 }

@@ -136,6 +136,47 @@ __device__ static inline void q4kv_prep_row(const float *in, float *out, const f
     }
 }
 
+/* byte k of w as a float (one v_cvt_f32_ubyte<k>) */
+__device__ static inline float q4kv_ubyte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xffu); }
+
+/* sum over the 4 biased bytes of w times x[0..3] */
+__device__ static inline float q4kv_dot4(uint32_t w, const float4 &x, float acc) {
+    w ^= 0x80808080u;
+    acc = fmaf(q4kv_ubyte_f(w, 0), x.x, acc);
+    acc = fmaf(q4kv_ubyte_f(w, 1), x.y, acc);
+    acc = fmaf(q4kv_ubyte_f(w, 2), x.z, acc);
+    acc = fmaf(q4kv_ubyte_f(w, 3), x.w, acc);
+    return acc;
+}
+
+/* One pair of q8_0 blocks (68 bytes as 17 dwords: blocks 2p, 2p+1 of a
+ * row) against x columns 64p .. 64p+63 (in LDS), given the two blocks'
+ * column sums xa, xb of x: d_a * sum(q x) + d_b * sum(q x). Each int8 is
+ * converted with v_cvt_f32_ubyte after flipping the sign bit (q + 128), and
+ * the block result is d * (S - 128 X). */
+__device__ static inline float q4kv_q8_pair_dot(const uint32_t (&dw)[17], const float *xs, uint32_t p,
+                                 float xa, float xb) {
+    const float4 *x4 = (const float4 *)(xs + 64u * p);
+    /* block A: fp16 d in bytes 0-1, quants in bytes 2..33 */
+    const float da = __half2float(__ushort_as_half((unsigned short)(dw[0] & 0xffffu)));
+    float sa = 0.f;
+    /* quants 0,1 are the high half of dw0; 2..29 in dw1..dw7; 30,31 low half of dw8 */
+    {
+        const uint32_t w0 = __builtin_amdgcn_perm(dw[1], dw[0], 0x05040302u); /* q0 q1 q2 q3 */
+        sa = q4kv_dot4(w0, x4[0], sa);
+#pragma unroll
+        for (int k = 1; k < 8; k++) {
+            const uint32_t wk = __builtin_amdgcn_perm(dw[k + 1], dw[k], 0x05040302u);
+            sa = q4kv_dot4(wk, x4[k], sa);
+        }
+    }
+    const float db = __half2float(__ushort_as_half((unsigned short)(dw[8] >> 16)));
+    float sb = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) sb = q4kv_dot4(dw[9 + k], x4[8 + k], sb);
+    return da * (sa - 128.f * xa) + db * (sb - 128.f * xb);
+}
+
 #define Q4KV_ERR(...)                                                          \
     do {                                                                       \
         fprintf(stderr, "q4 hip: " __VA_ARGS__);                               \

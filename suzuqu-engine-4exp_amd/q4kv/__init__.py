@@ -57,6 +57,12 @@ class PrepStepDesc(C.Structure):
 assert C.sizeof(PrepStepDesc) == 128
 
 
+class OutDesc(C.Structure):
+    """q4kv_out_desc of include/q4kv.h."""
+
+    _fields_ = [("w_o", _vp), ("y", _vp)]
+
+
 class AppendDesc(C.Structure):
     """q4kv_append_desc of include/q4kv.h (40 bytes)."""
 
@@ -116,6 +122,9 @@ SIGNATURES = {
     "q4_hip_qsa_topk_d": (_b, [_vp, _vp, _u32, _u32, _u32, _u32]),
     "q4_hip_qsa_step_prep_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32,
                                         _u32, _f32, _f32]),
+    "q4_hip_qsa_step_out_batch": (_b, [_vp, _vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32,
+                                       _u32, _f32]),
+    "q4_hip_gemv_dd": (_b, [_u32, _vp, _u64, _u64, _vp, _vp, _f32]),
     "q4kv_pipe_open": (_vp, [C.c_size_t]),
     "q4kv_pipe_close": (None, [_vp]),
     "q4kv_pipe_file_to_dev": (_b, [_vp, C.c_int, _u64, _vp, _u64]),

@@ -55,6 +55,8 @@ class Oracle:
         L.orc_qsa_score.argtypes = [vp, vp, vp, u32, u32, u32, u32, u32, u32, u32]
         L.orc_qsa_topk.restype = C.c_int
         L.orc_qsa_topk.argtypes = [vp, vp, u32, u32, u32, u32, u32, u32]
+        L.orc_gemv_q8_0.restype = C.c_int
+        L.orc_gemv_q8_0.argtypes = [vp, u64, u64, vp, vp, f32]
         L.orc_check_f16c.restype = u64
         L.orc_check_f16c.argtypes = [u64, u64, u64]
         self.ref = None
@@ -148,3 +150,10 @@ class Oracle:
         assert self.lib.orc_qsa_topk(_ptr(score), _ptr(sel), n_tok, stride, k_blk, ratio,
                                      pos0, width) == 0
         return sel
+
+    def gemv_q8(self, w, nrows, ncols, x, scale=1.0):
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(nrows, dtype=np.float32)
+        assert self.lib.orc_gemv_q8_0(_ptr(w), nrows, ncols, _ptr(x), _ptr(y), scale) == 0
+        return y

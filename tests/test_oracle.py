@@ -254,3 +254,28 @@ def test_selection_rule():
     assert mid.min() >= 3 and mid.max() <= pos - 512
     short = selection(rng, 100)
     assert list(short[:101]) == list(range(101)) and (short[101:] == -1).all()
+
+
+# --------------------------------------------------------------- q8_0 GEMV
+def test_gemv_q8_against_reference_dequant(oracle):
+    rng = np.random.default_rng(40)
+    nrows, ncols = 37, 320
+    wf = rng.standard_normal((nrows, ncols)).astype(np.float32)
+    w = oracle.quant_q8(wf)
+    x = rng.standard_normal(ncols).astype(np.float32)
+    y = oracle.gemv_q8(w, nrows, ncols, x, scale=0.5)
+    if oracle.ref is not None:   # the reference's own dequantiser
+        deq = np.empty(nrows * ncols, np.float32)
+        assert oracle.ref.q4_dequant_row(8, w.ctypes.data, nrows * ncols, deq.ctypes.data)
+        want = 0.5 * (deq.reshape(nrows, ncols).astype(np.float64) @ x.astype(np.float64))
+    else:
+        want = 0.5 * (oracle.dequant_q8(w, nrows * ncols).reshape(nrows, ncols).astype(np.float64)
+                      @ x.astype(np.float64))
+    np.testing.assert_allclose(y, want, rtol=1e-6, atol=1e-5)
+    # closed form: a weight row with one +-1 per block... row r = e_{c} picks x[c] (scale 1/127)
+    e = np.zeros((3, ncols), np.float32)
+    for r, c in enumerate((0, 77, 319)):
+        e[r, c] = 1.0
+    ye = oracle.gemv_q8(oracle.quant_q8(e), 3, ncols, x)
+    d = np.float32(np.float16(1.0 / 127)) * 127
+    np.testing.assert_allclose(ye, d * x[[0, 77, 319]], rtol=1e-6)
