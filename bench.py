@@ -754,6 +754,10 @@ def config_indexer(b, steps=100, layers=12):
     return out
 
 
+ONLY = {"config2": config2, "config3": config3, "config4": config4, "prep": config_prep,
+        "out": config_out, "indexer": config_indexer}
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -777,6 +781,9 @@ def main():
                     help="also measure configs 2, 3 and 4 (0 to skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a device-to-device copy of MIB MiB (PMC calibration)")
+    ap.add_argument("--only", choices=sorted(ONLY), default=None,
+                    help="only measure one of the extra configurations and print its JSON "
+                         "(for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the QSA KV path runs on a single MI355X "
@@ -790,6 +797,10 @@ def main():
             assert rt.lib.q4_hip_copy(dst, src, n // 4)
         rt.sync()
         print(json.dumps({"copy_bytes": n, "launches": 3}))
+        return
+    if args.only:
+        b = Bench(args.layers, max(args.sets, 4))
+        print(json.dumps({args.only: ONLY[args.only](b)}), flush=True)
         return
     b = Bench(args.layers, args.sets)
     res = {}
