@@ -754,8 +754,67 @@ def config_indexer(b, steps=100, layers=12):
     return out
 
 
+def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
+    """The indexer of config 3's chunked prefill (src/q4_fwd.c:740-770, sliced by 512
+    tokens as src/q4_fwd.c:1744-1754): for each 512-token slice of an 8192-token
+    chunk after a 16384-token cache, the indexer queries' RMSNorm + RoPE
+    (q4_hip_qsa_k_prep_n), the scores of every visible block (fp32 MFMA), and the
+    top-512 selection of every token expanded to 2051 positions. The pool of all
+    6144 blocks is rebuilt first (q4_hip_qsa_pool), as a new chunk's keys arrive."""
+    rt, lib = b.rt, b.lib
+    n_pos = cache + chunk
+    nb = n_pos // IDX_RATIO
+    raw = rt.alloc(n_pos * IDX_DIM * 2)
+    tmp = rt.alloc(max(n_pos * IDX_DIM, chunk * IDX_HEADS * IDX_DIM) * 4)
+    b.gen(tmp, n_pos * IDX_DIM, 9300)
+    assert lib.q4_hip_f32_to_f16(raw, tmp, n_pos * IDX_DIM)
+    pool = rt.alloc(nb * IDX_DIM * 4)
+    wn = rt.alloc(IDX_DIM * 4)
+    b.gen(wn, IDX_DIM, 9301)
+    q = rt.alloc(chunk * IDX_HEADS * IDX_DIM * 4)
+    score = rt.alloc(slice_ * nb * 4)
+    sel = rt.alloc(slice_ * WIDTH * 4)
+    rt.sync()
+
+    def run():
+        ok = lib.q4_hip_qsa_pool(raw, pool, wn, IDX_DIM, IDX_RATIO, 0, nb, IDX_ROT, IDX_BASE,
+                                 IDX_EPS)
+        for s0 in range(0, chunk, slice_):
+            pos0 = cache + s0
+            qs = q + s0 * IDX_HEADS * IDX_DIM * 4
+            ok &= lib.q4_hip_copy(qs, tmp + s0 * IDX_HEADS * IDX_DIM * 4,
+                                  slice_ * IDX_HEADS * IDX_DIM)
+            ok &= lib.q4_hip_qsa_k_prep_n(qs, wn, IDX_HEADS, IDX_DIM, IDX_ROT, pos0, IDX_BASE,
+                                          IDX_EPS, slice_)
+            n_blocks = (pos0 + slice_) // IDX_RATIO
+            ok &= lib.q4_hip_qsa_score(qs, pool, score, slice_, n_blocks, nb, IDX_HEADS,
+                                       IDX_DIM, pos0, IDX_RATIO)
+            ok &= lib.q4_hip_qsa_topk(score, sel, slice_, n_blocks, nb, IDX_KBLK, IDX_RATIO,
+                                      pos0, WIDTH)
+        return ok
+
+    b.gen(tmp, chunk * IDX_HEADS * IDX_DIM, 9302)
+    assert run()
+    rt.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        assert run()
+    rt.sync()
+    t = (time.perf_counter() - t0) / reps
+    flop = sum(2.0 * slice_ * IDX_HEADS * IDX_DIM * ((cache + s0 + slice_) // IDX_RATIO)
+               for s0 in range(0, chunk, slice_))
+    for p_ in (raw, tmp, pool, wn, q, score, sel):
+        rt.free(p_)
+    return {"what": f"indexer of an {chunk}-token prefill chunk after a {cache}-token cache, "
+                    f"{slice_}-token slices: pool rebuild ({nb} blocks), query prep, scores "
+                    "(fp32 MFMA), top-512 + expansion per token",
+            "us_per_layer": round(t * 1e6, 1), "us_per_token": round(t * 1e6 / chunk, 3),
+            "score_gflop": round(flop / 1e9, 1)}
+
+
 ONLY = {"config2": config2, "config3": config3, "config4": config4, "prep": config_prep,
-        "out": config_out, "indexer": config_indexer}
+        "out": config_out, "indexer": config_indexer,
+        "indexer_prefill": config_indexer_prefill}
 
 
 def _cpu_model():
@@ -817,7 +876,8 @@ def main():
                    "config4_widths_restore": config4(b),
                    "qk_prep_fused_step": config_prep(b),
                    "out_projection_fused": config_out(b),
-                   "indexer_decode": config_indexer(b)}
+                   "indexer_decode": config_indexer(b),
+                   "indexer_prefill": config_indexer_prefill(b)}
     threads = min(16, os.cpu_count() or 1)
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
     head = "batched" if "batched" in res else "sequential"
