@@ -20,9 +20,10 @@
  *   score  decode: a memory-bound stream over the pool (512 B per block);
  *          eight lanes per block row, each lane holding 16 dims of all four
  *          queries in registers, a 3-step DPP reduction per head.
- *          prefill (>= 4 tokens): fp32 MFMA 16x16x4 with A rows (token, head)
- *          so each lane's four accumulators are one token's four heads and
- *          the relu-sum over heads stays in the lane.
+ *          prefill (>= 4 tokens): bf16 MFMA 16x16x32 with a three-product
+ *          hi/lo split (~2^-16 relative per product), A rows (token, head) so
+ *          each lane's four accumulators are one token's four heads and the
+ *          relu-sum over heads stays in the lane.
  *   topk   one 1024-thread workgroup per token row, keys in VGPRs (64 per
  *          thread). One histogram pass of the distance from the row maximum
  *          (1/16-octave steps of |score|, 32-way replicated LDS counters so
@@ -285,13 +286,35 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
 
-/* Block scores for a chunk of >= 4 tokens on fp32 MFMA (16x16x4). A tile =
- * 4 tokens x 4 heads (row 4*token + head), B tile = 16 pool rows. The dot
- * product's dims are permuted so each lane reads 32 contiguous floats of its
- * row: at step s, lane l contributes dim 32*(l/16) + s. The C layout puts one
- * token's four heads in a lane's four accumulators. Workgroup tile: 16 tokens
- * x 256 blocks, 64 blocks per wave. */
+/* fp32 -> (hi, lo) bf16 pairs, both by truncation: hi = x's top 16 bits,
+ * lo = the top 16 bits of x - hi (exact in fp32), so x = hi + lo to within
+ * 2^-16 |x|. Two values per dword, low half first. */
+__device__ inline void split_bf16(const float4 &a, const float4 &b, s16x8 &hi, s16x8 &lo) {
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t u0 = __float_as_uint(v[2 * i]), u1 = __float_as_uint(v[2 * i + 1]);
+        const uint32_t h0 = u0 & 0xffff0000u, h1 = u1 & 0xffff0000u;
+        const uint32_t l0 = __float_as_uint(v[2 * i] - __uint_as_float(h0));
+        const uint32_t l1 = __float_as_uint(v[2 * i + 1] - __uint_as_float(h1));
+        h[i] = __builtin_amdgcn_perm(h1, h0, 0x07060302u); /* {h0.hi16, h1.hi16} */
+        l[i] = __builtin_amdgcn_perm(l1, l0, 0x07060302u);
+    }
+    hi = __builtin_bit_cast(s16x8, (uint4){h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(s16x8, (uint4){l[0], l[1], l[2], l[3]});
+}
+
+/* Block scores for a chunk of >= 4 tokens on bf16 MFMA 16x16x32 with a
+ * three-product split (hi.hi + hi.lo + lo.hi, relative error ~2^-16 per
+ * product, fp32 accumulation). A tile = 4 tokens x 4 heads (row 4*token +
+ * head), B tile = 16 pool rows; at k-step s lane l supplies dims
+ * 32s + 8(l/16) .. +7 of its row (32 contiguous bytes: a row's 128 bytes per
+ * step come from its four lanes). The C layout puts one token's four heads in
+ * a lane's four accumulators, so the relu-sum over heads stays in the lane.
+ * Workgroup tile: 16 tokens x 256 blocks, 64 blocks per wave. */
 __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const float *pool,
                                                         float *score, uint32_t n_tok,
                                                         uint32_t n_blocks, uint32_t stride,
@@ -309,14 +332,14 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
     for (int a = 0; a < 4; a++) {
         const uint32_t tok = tok0 + 4u * a + (i16 >> 2), head = i16 & 3u;
         av[a] = tok < n_tok && head < n_head;
-        ap[a] = q + ((size_t)(av[a] ? tok : 0) * n_head + (av[a] ? head : 0)) * IDX_HD + 32u * kq;
+        ap[a] = q + ((size_t)(av[a] ? tok : 0) * n_head + (av[a] ? head : 0)) * IDX_HD + 8u * kq;
     }
     const float *bp[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         uint32_t blk = blk0 + 16u * b + i16;
         blk = blk < n_blocks ? blk : n_blocks - 1;
-        bp[b] = pool + (size_t)blk * IDX_HD + 32u * kq;
+        bp[b] = pool + (size_t)blk * IDX_HD + 8u * kq;
     }
     f32x4 acc[4][4];
 #pragma unroll
@@ -324,33 +347,30 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll 1
-    for (uint32_t kc = 0; kc < 32; kc += 8) {
-        float4 A[4][2], B[4][2];
+#pragma unroll
+    for (uint32_t st = 0; st < 4; st++) {
+        s16x8 Ah[4], Al[4], Bh[4], Bl[4];
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 x0 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * st)) : z;
+            const float4 x1 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * st) + 1) : z;
+            split_bf16(x0, x1, Ah[a], Al[a]);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float4 y0 = ld_vec((const float4 *)(bp[b] + 32u * st));
+            const float4 y1 = ld_vec((const float4 *)(bp[b] + 32u * st) + 1);
+            split_bf16(y0, y1, Bh[b], Bl[b]);
+        }
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int h = 0; h < 2; h++)
-                A[a][h] = av[a] ? ld_vec((const float4 *)(ap[a] + kc) + h)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int b = 0; b < 4; b++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) B[b][h] = ld_vec((const float4 *)(bp[b] + kc) + h);
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-#pragma unroll
-            for (int a = 0; a < 4; a++) {
-                const float4 &av4 = A[a][s >> 2];
-                const float x = (s & 3) == 0 ? av4.x : (s & 3) == 1 ? av4.y : (s & 3) == 2 ? av4.z : av4.w;
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const float4 &bv4 = B[b][s >> 2];
-                    const float y = (s & 3) == 0 ? bv4.x : (s & 3) == 1 ? bv4.y : (s & 3) == 2 ? bv4.z : bv4.w;
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc[a][b], 0, 0, 0);
-                }
+            for (int b = 0; b < 4; b++) {
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al[a], Bh[b], acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[a], Bl[b], acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[a], Bh[b], acc[a][b], 0, 0, 0);
             }
-        }
     }
     /* lane holds C[4*kq + r][i16]: token tok0 + 4a + kq, head r, block blk0 + 16b + i16 */
 #pragma unroll
