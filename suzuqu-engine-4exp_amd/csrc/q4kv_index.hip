@@ -395,8 +395,7 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
 /* --------------------------------------------------------------- topk ---- */
 
 constexpr uint32_t TK_T = 1024;        /* threads per row workgroup */
-constexpr uint32_t TK_KPT = 64;        /* register-resident keys per thread */
-constexpr uint32_t TK_CHUNK = TK_T * TK_KPT;
+constexpr uint32_t TK_KPT = 64;        /* register-resident keys per thread (long rows) */
 constexpr uint32_t TK_MAXK = 512;      /* largest k_blk */
 constexpr uint32_t TK_CAP = 4096;      /* candidate list capacity */
 constexpr uint32_t TK_DSHIFT = 19;     /* coarse bins: 1/16 octave of |score| */
@@ -499,8 +498,9 @@ __device__ inline uint32_t lanes_below(uint64_t m) {
 /* One token row: exact top-`need` blocks by (key desc, index asc), emitted
  * above-threshold ascending then threshold ties ascending, expanded to sel.
  * Same list as src/q4_rocm.cu:7736-7846 (and the device-position pipeline
- * :7505-7696). Keys of row element e = c*TK_CHUNK + r*TK_T + tid live in
- * key[r] during chunk c.
+ * :7505-7696). Keys of row element e = c*TK_T*KPT + r*TK_T + tid live in
+ * key[r] during chunk c (KPT keys per thread: 16 for rows of up to 16384
+ * blocks, 64 for longer ones).
  *
  * Fast path (rows of <= 65536 blocks): one histogram pass of the distance
  * from the row maximum finds the bin holding the need-th key; every key in
@@ -509,7 +509,7 @@ __device__ inline uint32_t lanes_below(uint64_t m) {
  * exact threshold is found by 12-bit radix passes over them alone.
  * Otherwise (long rows, heavy ties) the full path runs four 8-bit radix
  * passes over all keys and an ordered compaction of all keys. */
-template <bool DEV>
+template <bool DEV, uint32_t KPT>
 __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *sel,
                                                    uint32_t stride, uint32_t k_blk,
                                                    uint32_t ratio, uint32_t pos0,
@@ -526,8 +526,9 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         return;
     }
     const float *row = score + (size_t)t * stride;
+    constexpr uint32_t TK_CHUNK = TK_T * KPT;
     const uint32_t nchunk = (n_vis + TK_CHUNK - 1) / TK_CHUNK;
-    uint32_t key[TK_KPT];
+    uint32_t key[KPT];
     /* Elements past n_vis get key 0, the smallest key. Since need <= n_vis
      * they sort below the need-th largest real key (or tie with it only when
      * that key is 0), so the radix passes need no validity test; the
@@ -537,10 +538,10 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         const uint32_t lim = n_vis - c * TK_CHUNK;
         if (lim >= TK_CHUNK) {
 #pragma unroll
-            for (uint32_t r = 0; r < TK_KPT; r++) key[r] = xkey(ldg(src + r * TK_T));
+            for (uint32_t r = 0; r < KPT; r++) key[r] = xkey(ldg(src + r * TK_T));
         } else {
 #pragma unroll
-            for (uint32_t r = 0; r < TK_KPT; r++)
+            for (uint32_t r = 0; r < KPT; r++)
                 key[r] = r * TK_T + tid < lim ? xkey(ldg(src + r * TK_T)) : 0u;
         }
     };
@@ -554,7 +555,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         /* ---- row maximum (as the loads land) ---- */
         uint32_t mx = 0;
 #pragma unroll
-        for (uint32_t r = 0; r < TK_KPT; r++) mx = max(mx, key[r]);
+        for (uint32_t r = 0; r < KPT; r++) mx = max(mx, key[r]);
         mx = wave_max_u32(mx);
         if (lane == 0) sm.wtot[1][wave] = mx;
         __syncthreads();
@@ -567,7 +568,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         const uint32_t Mb = M >> TK_DSHIFT;
         uint32_t *hc = sm.h.dist + (lane & 31u);
 #pragma unroll
-        for (uint32_t r = 0; r < TK_KPT; r++)
+        for (uint32_t r = 0; r < KPT; r++)
             atomicAdd(hc + min(Mb - (key[r] >> TK_DSHIFT), TK_DBINS - 1u) * 32u, 1u);
         __syncthreads();
         { /* fold the copies: two threads per bin */
@@ -606,9 +607,9 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
              * (the full key is fetched again from the row, an L2 hit) ---- */
             uint32_t mlo = 0, mhi = 0;
 #pragma unroll
-            for (uint32_t r = 0; r < 32; r++) mlo |= key[r] >= Kc ? 1u << r : 0u;
+            for (uint32_t r = 0; r < (KPT < 32 ? KPT : 32); r++) mlo |= key[r] >= Kc ? 1u << r : 0u;
 #pragma unroll
-            for (uint32_t r = 0; r < 32; r++) mhi |= key[32 + r] >= Kc ? 1u << r : 0u;
+            for (uint32_t r = 32; r < KPT; r++) mhi |= key[r] >= Kc ? 1u << (r - 32) : 0u;
             const uint64_t mine0 = ((uint64_t)mhi << 32) | mlo;
             for (uint64_t m = mine0; m; m &= m - 1ull)
                 atomicOr(&sm.wm[(uint32_t)__builtin_ctzll(m) * 16u + wave], 1ull << lane);
@@ -701,7 +702,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
             for (uint32_t c = 0; c < nchunk; c++) {
                 if (nchunk > 1) load_chunk(c);
 #pragma unroll
-                for (uint32_t r = 0; r < TK_KPT; r++) {
+                for (uint32_t r = 0; r < KPT; r++) {
                     const uint32_t u = key[r];
                     /* digits above this pass must equal the prefix found so
                      * far (pass 0: the empty prefix, (u >> 8) >> 24 == 0) */
@@ -746,7 +747,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         for (uint32_t c = 0; c < nchunk; c++) {
             if (nchunk > 1) load_chunk(c);
             uint32_t gv = 0, ev = 0;
-            unroll<TK_KPT>([&](auto rc) {
+            unroll<KPT>([&](auto rc) {
                 constexpr uint32_t r = rc;
                 const uint32_t ng = (uint32_t)__popcll(__ballot(key[r] > thr));
                 const uint32_t ne = (uint32_t)__popcll(
@@ -767,7 +768,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
             uint32_t thr2 = thr;
             asm volatile("" : "+v"(thr2)); /* do not carry the first loop's masks */
 #pragma unroll
-            for (uint32_t r = 0; r < TK_KPT; r++) {
+            for (uint32_t r = 0; r < KPT; r++) {
                 const bool gt = key[r] > thr2;
                 const bool eq = (key[r] == thr2) & ((thr2 != 0u) | valid(c, r));
                 const uint64_t bg = __ballot(gt), be = __ballot(eq);
@@ -995,8 +996,14 @@ extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok
         width == 0 || ratio == 0)
         return false;
     (void)hipGetLastError();
-    qsa_topk_k<false><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk, ratio, pos0,
-                                                        width, nullptr);
+    /* the longest row decides the register layout */
+    const uint64_t vis_max = ((uint64_t)pos0 + n_tok) / ratio;
+    if (vis_max <= 16u * TK_T)
+        qsa_topk_k<false, 16><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk, ratio,
+                                                                pos0, width, nullptr);
+    else
+        qsa_topk_k<false, TK_KPT><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk,
+                                                                    ratio, pos0, width, nullptr);
     return q4kv_launch_ok("qsa_topk");
 }
 extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride,
@@ -1004,10 +1011,15 @@ extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t str
     if (!q4kv_ok || !q4kv_pos_d || !score || !sel || k_blk == 0 || k_blk > TK_MAXK ||
         width == 0 || ratio == 0)
         return false;
-    (void)stride;
     (void)hipGetLastError();
-    qsa_topk_k<true><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0, width,
-                                                   q4kv_pos_d);
+    /* the device position is unknown here: the row capacity (stride blocks)
+     * decides the register layout; 0 means unknown */
+    if (stride && stride <= 16u * TK_T)
+        qsa_topk_k<true, 16><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0, width,
+                                                           q4kv_pos_d);
+    else
+        qsa_topk_k<true, TK_KPT><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0,
+                                                               width, q4kv_pos_d);
     return q4kv_launch_ok("qsa_topk_d");
 }
 
