@@ -734,9 +734,22 @@ def config_indexer(b, steps=100, layers=12):
                                             WIDTH)
         return ok
 
+    descs = (q4kv.IndexDesc * layers)()
+    for li in range(layers):
+        descs[li] = q4kv.IndexDesc(raws[li], pools[li], wn, ks[li], qs[li], wn, scs[li],
+                                   sels[li], pos)
+    dd = rt.alloc(C.sizeof(descs))
+    assert lib.q4_hip_h2d(dd, C.addressof(descs), C.sizeof(descs))
+
+    def batched(r):
+        return lib.q4_hip_qsa_index_batch(dd, layers, max_blocks, IDX_HEADS, IDX_DIM, IDX_RATIO,
+                                          IDX_ROT, IDX_BASE, IDX_EPS, IDX_KBLK, WIDTH)
+
     out = {"what": f"decode indexer, {layers} layers x 65536 visible blocks (ctx {CTX}), "
                    "4 heads x 128 dims, top-512 of 4-position blocks -> 2051 positions",
-           "launches_per_layer": {"full": 5, "fused": 2}}
+           "launches_per_layer": {"full": 5, "fused": 2, "batched": 2.0 / layers}}
+    graphs = _graphs(lib, batched, 2)
+    out["batched_us_per_layer"] = round(_time_graphs(b, graphs, steps) / layers * 1e6, 3)
     for name, parts in (("full", ("store", "prep", "score", "topk")), ("score", ("score",)),
                         ("topk", ("topk",)), ("fused", ("fused", "topk"))):
         graphs = _graphs(lib, lambda r: step(parts), 2)
@@ -749,7 +762,7 @@ def config_indexer(b, steps=100, layers=12):
     out["pool_rebuild_ms"] = round(t_pool * 1e3, 3)
     pool_b = CTX * IDX_DIM * 2 + max_blocks * IDX_DIM * 4
     out["pool_rebuild_gbs"] = round(pool_b / t_pool / 1e9, 1)
-    for p_ in raws + pools + scs + sels + qs + ks + [wn]:
+    for p_ in raws + pools + scs + sels + qs + ks + [wn, dd]:
         rt.free(p_)
     return out
 

@@ -243,6 +243,31 @@ bool q4_hip_qsa_index_score_d(void *raw_f16, float *pool, const float *wn_k, con
                               uint32_t n_head, uint32_t hd, uint32_t ratio, uint32_t n_rot,
                               float rope_base, float eps);
 
+/* One item of a batched decode indexer step: an independent sequence (or
+ * layer) with its own indexer buffers and position. Device pointers; the
+ * descriptor array lives in device memory. 80 bytes. */
+typedef struct {
+    void *raw;           /* fp16 raw keys [max_kv][hd]; row pos is written */
+    float *pool;         /* fp32 pooled blocks [max_kv/ratio][hd] */
+    const float *wn_k;   /* k_norm weights [hd] or NULL */
+    const float *k_new;  /* the token's raw indexer key, fp32 [hd] */
+    const float *q;      /* raw indexer queries, fp32 [n_head][hd] (read, not modified) */
+    const float *wn_q;   /* q_norm weights [hd] or NULL */
+    float *score;        /* fp32 [max_blocks] scores (written) */
+    int32_t *sel;        /* int32 [width] position list (written) */
+    uint32_t pos;        /* the token's position */
+    uint32_t reserved[3];
+} q4kv_index_desc;
+
+/* The decode indexer of n_items independent items in two launches: per item
+ * the effect of q4_hip_qsa_index_score_d then q4_hip_qsa_topk_d at the item's
+ * own position (the same bytes as those calls; tests/test_gpu_index.py).
+ * max_blocks bounds every item's visible blocks (the score grid). */
+bool q4_hip_qsa_index_batch(const q4kv_index_desc *d_descs, uint32_t n_items,
+                            uint32_t max_blocks, uint32_t n_head, uint32_t hd, uint32_t ratio,
+                            uint32_t n_rot, float rope_base, float eps, uint32_t k_blk,
+                            uint32_t width);
+
 /* Append into n_desc caches in one launch (the per-layer
  * q4_hip_kv_append_d of a decode step, batched). */
 bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc, uint32_t n,

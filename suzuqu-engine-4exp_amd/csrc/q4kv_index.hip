@@ -230,16 +230,31 @@ __global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float
  * completes pools it (with the new key's fp16 row in place of the stored
  * one) and writes it to the pool; then every workgroup scores its 64 rows.
  * q is read, not modified. */
+template <bool BATCH>
 __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float *pool,
                                                           const float *wn_k, const float *k_new,
                                                           const float *q, const float *wn_q,
                                                           float *score, uint32_t n_head,
                                                           uint32_t ratio, uint32_t n_rot,
                                                           float base, float eps,
-                                                          const int32_t *pp) {
+                                                          const int32_t *pp,
+                                                          const q4kv_index_desc *descs) {
     __shared__ float qs[4][IDX_HD];
     __shared__ float new_row[IDX_HD];
-    const uint32_t pos = (uint32_t)*pp;
+    uint32_t pos;
+    if (BATCH) { /* item blockIdx.y of a batch: its own buffers and position */
+        const q4kv_index_desc *d = descs + blockIdx.y;
+        raw2 = (uint32_t *)ldg(&d->raw);
+        pool = ldg(&d->pool);
+        wn_k = ldg(&d->wn_k);
+        k_new = ldg(&d->k_new);
+        q = ldg(&d->q);
+        wn_q = ldg(&d->wn_q);
+        score = ldg(&d->score);
+        pos = ldg(&d->pos);
+    } else {
+        pos = (uint32_t)*pp;
+    }
     const uint32_t n_vis = (pos + 1) / ratio;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t rb = blockIdx.x * SC_ROWS_WG;
@@ -509,23 +524,38 @@ __device__ inline uint32_t lanes_below(uint64_t m) {
  * exact threshold is found by 12-bit radix passes over them alone.
  * Otherwise (long rows, heavy ties) the full path runs four 8-bit radix
  * passes over all keys and an ordered compaction of all keys. */
-template <bool DEV, uint32_t KPT>
+/* Where a row comes from: token rows pos0 + t of one score matrix, the
+ * device position's single row, or item t of a batch of descriptors. */
+enum { TK_ROWS = 0, TK_DEV = 1, TK_BATCH = 2 };
+
+template <int SRC, uint32_t KPT>
 __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *sel,
                                                    uint32_t stride, uint32_t k_blk,
                                                    uint32_t ratio, uint32_t pos0,
-                                                   uint32_t width, const int32_t *pp) {
+                                                   uint32_t width, const int32_t *pp,
+                                                   const q4kv_index_desc *descs) {
     __shared__ TopkSmem sm;
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
-    const uint32_t pos = (DEV ? (uint32_t)*pp : pos0) + t;
+    uint32_t pos;
+    const float *row;
+    int32_t *out;
+    if (SRC == TK_BATCH) {
+        const q4kv_index_desc *d = descs + t;
+        pos = ldg(&d->pos);
+        row = ldg(&d->score);
+        out = ldg(&d->sel);
+    } else {
+        pos = (SRC == TK_DEV ? (uint32_t)*pp : pos0) + t;
+        row = score + (size_t)t * stride;
+        out = sel + (size_t)t * width;
+    }
     const uint32_t n_vis = (pos + 1) / ratio;
     const uint32_t need = n_vis < k_blk ? n_vis : k_blk;
-    int32_t *out = sel + (size_t)t * width;
     if (need == n_vis) { /* every complete block fits: the dense prefix */
         for (uint32_t w = tid; w < width; w += TK_T) out[w] = w <= pos ? (int32_t)w : -1;
         return;
     }
-    const float *row = score + (size_t)t * stride;
     constexpr uint32_t TK_CHUNK = TK_T * KPT;
     const uint32_t nchunk = (n_vis + TK_CHUNK - 1) / TK_CHUNK;
     uint32_t key[KPT];
@@ -999,11 +1029,12 @@ extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok
     /* the longest row decides the register layout */
     const uint64_t vis_max = ((uint64_t)pos0 + n_tok) / ratio;
     if (vis_max <= 16u * TK_T)
-        qsa_topk_k<false, 16><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk, ratio,
-                                                                pos0, width, nullptr);
+        qsa_topk_k<TK_ROWS, 16><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk,
+                                                                  ratio, pos0, width, nullptr,
+                                                                  nullptr);
     else
-        qsa_topk_k<false, TK_KPT><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk,
-                                                                    ratio, pos0, width, nullptr);
+        qsa_topk_k<TK_ROWS, TK_KPT><<<n_tok, TK_T, 0, q4kv_stream>>>(
+            score, sel, stride, k_blk, ratio, pos0, width, nullptr, nullptr);
     return q4kv_launch_ok("qsa_topk");
 }
 extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride,
@@ -1015,11 +1046,11 @@ extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t str
     /* the device position is unknown here: the row capacity (stride blocks)
      * decides the register layout; 0 means unknown */
     if (stride && stride <= 16u * TK_T)
-        qsa_topk_k<true, 16><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0, width,
-                                                           q4kv_pos_d);
+        qsa_topk_k<TK_DEV, 16><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0,
+                                                             width, q4kv_pos_d, nullptr);
     else
-        qsa_topk_k<true, TK_KPT><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0,
-                                                               width, q4kv_pos_d);
+        qsa_topk_k<TK_DEV, TK_KPT><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0,
+                                                                 width, q4kv_pos_d, nullptr);
     return q4kv_launch_ok("qsa_topk_d");
 }
 
@@ -1039,8 +1070,31 @@ extern "C" bool q4_hip_qsa_index_score_d(void *raw_f16, float *pool, const float
     if (stride == 0) return true;
     (void)hipGetLastError();
     const uint32_t gx = (stride + SC_ROWS_WG - 1) / SC_ROWS_WG;
-    qsa_index_score_dk<<<gx, 256, 0, q4kv_stream>>>((uint32_t *)raw_f16, pool, wn_k, k_new, q,
-                                                    wn_q, score, n_head, ratio, n_rot,
-                                                    rope_base, eps, q4kv_pos_d);
+    qsa_index_score_dk<false><<<gx, 256, 0, q4kv_stream>>>((uint32_t *)raw_f16, pool, wn_k,
+                                                           k_new, q, wn_q, score, n_head, ratio,
+                                                           n_rot, rope_base, eps, q4kv_pos_d,
+                                                           nullptr);
     return q4kv_launch_ok("qsa_index_score_d");
+}
+
+extern "C" bool q4_hip_qsa_index_batch(const q4kv_index_desc *d_descs, uint32_t n_items,
+                                       uint32_t max_blocks, uint32_t n_head, uint32_t hd,
+                                       uint32_t ratio, uint32_t n_rot, float rope_base, float eps,
+                                       uint32_t k_blk, uint32_t width) {
+    if (!q4kv_ok || !d_descs || n_items == 0 || n_items > 65535u || max_blocks == 0 ||
+        hd != IDX_HD || n_head == 0 || n_head > 4 || ratio == 0 || n_rot > hd || k_blk == 0 ||
+        k_blk > TK_MAXK || width == 0)
+        return false;
+    (void)hipGetLastError();
+    const uint32_t gx = (max_blocks + SC_ROWS_WG - 1) / SC_ROWS_WG;
+    qsa_index_score_dk<true><<<dim3(gx, n_items), 256, 0, q4kv_stream>>>(
+        nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, n_head, ratio, n_rot,
+        rope_base, eps, nullptr, d_descs);
+    if (max_blocks <= 16u * TK_T)
+        qsa_topk_k<TK_BATCH, 16><<<n_items, TK_T, 0, q4kv_stream>>>(
+            nullptr, nullptr, 0, k_blk, ratio, 0, width, nullptr, d_descs);
+    else
+        qsa_topk_k<TK_BATCH, TK_KPT><<<n_items, TK_T, 0, q4kv_stream>>>(
+            nullptr, nullptr, 0, k_blk, ratio, 0, width, nullptr, d_descs);
+    return q4kv_launch_ok("qsa_index_batch");
 }

@@ -63,6 +63,17 @@ class OutDesc(C.Structure):
     _fields_ = [("w_o", _vp), ("y", _vp)]
 
 
+class IndexDesc(C.Structure):
+    """q4kv_index_desc of include/q4kv.h (80 bytes)."""
+
+    _fields_ = [("raw", _vp), ("pool", _vp), ("wn_k", _vp), ("k_new", _vp), ("q", _vp),
+                ("wn_q", _vp), ("score", _vp), ("sel", _vp), ("pos", _u32),
+                ("reserved", _u32 * 3)]
+
+
+assert C.sizeof(IndexDesc) == 80
+
+
 class AppendDesc(C.Structure):
     """q4kv_append_desc of include/q4kv.h (40 bytes)."""
 
@@ -130,6 +141,8 @@ SIGNATURES = {
     "q4kv_pipe_file_to_dev": (_b, [_vp, C.c_int, _u64, _vp, _u64]),
     "q4kv_pipe_dev_to_file": (_b, [_vp, C.c_int, _u64, _vp, _u64]),
     "q4kv_pipe_finish": (_b, [_vp]),
+    "q4_hip_qsa_index_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _f32, _f32, _u32,
+                                    _u32]),
     "q4_hip_qsa_index_score_d": (_b, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                       _u32, _f32, _f32]),
     "q4_hip_qsa_decode_n": (_b, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,

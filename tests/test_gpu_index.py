@@ -374,3 +374,64 @@ def test_fused_index_score_matches_separate_calls(rt, pos):
     assert np.array_equal(s0.view(np.uint32), s1.view(np.uint32))
     assert np.array_equal(l0, l1)
     assert np.array_equal(q1.reshape(q.shape), q)      # q untouched by the fused call
+
+
+def test_index_batch_matches_per_item_calls(rt):
+    """q4_hip_qsa_index_batch == per item q4_hip_qsa_index_score_d +
+    q4_hip_qsa_topk_d at the item's position, bit for bit, for items of
+    different lengths (dense-prefix, completing and non-completing blocks)."""
+    import ctypes
+    import q4kv
+    lib = rt.lib
+    rng = np.random.default_rng(77)
+    max_kv = 65536 * 4
+    max_blocks = max_kv // RATIO
+    positions = [2, 1500, 40003, 100007, max_kv - 1]
+    items = []
+    for pos in positions:
+        items.append(dict(pos=pos, raw=raw_keys(rng, max_kv),
+                          pool=(rng.standard_normal((max_blocks, IDX_DIM)) * 0.3).astype(np.float32),
+                          k=rng.standard_normal(IDX_DIM).astype(np.float32),
+                          q=rng.standard_normal((IDX_HEADS, IDX_DIM)).astype(np.float32),
+                          wk=(1 + 0.2 * rng.standard_normal(IDX_DIM)).astype(np.float32),
+                          wq=(1 + 0.2 * rng.standard_normal(IDX_DIM)).astype(np.float32)))
+    results = []
+    for batched in (True, False):
+        note(f"index batch batched={batched}")
+        descs = (q4kv.IndexDesc * len(items))()
+        ptrs = []
+        for i, it in enumerate(items):
+            d = dict(raw=rt.upload(it["raw"]), pool=rt.upload(it["pool"]), wk=rt.upload(it["wk"]),
+                     k=rt.upload(it["k"]), q=rt.upload(it["q"]), wq=rt.upload(it["wq"]),
+                     sc=rt.upload(np.full(max_blocks, np.nan, np.float32)), sel=rt.alloc(WIDTH * 4))
+            ptrs.append(d)
+            descs[i] = q4kv.IndexDesc(d["raw"], d["pool"], d["wk"], d["k"], d["q"], d["wq"],
+                                      d["sc"], d["sel"], it["pos"])
+            if not batched:
+                lib.q4_hip_pos_push(it["pos"])
+                assert lib.q4_hip_qsa_index_score_d(d["raw"], d["pool"], d["wk"], d["k"], d["q"],
+                                                    d["wq"], d["sc"], max_blocks, IDX_HEADS,
+                                                    IDX_DIM, RATIO, N_ROT, ROPE_BASE, RMS_EPS)
+                assert lib.q4_hip_qsa_topk_d(d["sc"], d["sel"], max_blocks, K_BLK, RATIO, WIDTH)
+        if batched:
+            dd = rt.alloc(ctypes.sizeof(descs))
+            assert lib.q4_hip_h2d(dd, ctypes.addressof(descs), ctypes.sizeof(descs))
+            assert lib.q4_hip_qsa_index_batch(dd, len(items), max_blocks, IDX_HEADS, IDX_DIM,
+                                              RATIO, N_ROT, ROPE_BASE, RMS_EPS, K_BLK, WIDTH)
+        rt.sync()
+        res = []
+        for d, it in zip(ptrs, items):
+            n_vis = (it["pos"] + 1) // RATIO
+            res.append((rt.download(d["raw"], it["raw"].nbytes, np.uint16)[
+                            it["pos"] * IDX_DIM:(it["pos"] + 1) * IDX_DIM],
+                        rt.download(d["pool"], it["pool"].nbytes, np.float32),
+                        rt.download(d["sc"], max_blocks * 4, np.float32)[:n_vis],
+                        rt.download(d["sel"], WIDTH * 4, np.int32)))
+            for p in d.values():
+                rt.free(p)
+        if batched:
+            rt.free(dd)
+        results.append(res)
+    for i, (a, b) in enumerate(zip(*results)):
+        for j in range(4):
+            assert np.array_equal(a[j].view(np.uint8), b[j].view(np.uint8)), (positions[i], j)
