@@ -738,6 +738,29 @@ __device__ static inline uint32_t q8_col_of_dim(uint32_t d) {
  * qsa_attn_k with every shape constant compile-time, the weight hi/lo split
  * done with mixed-precision FMAs, and the partial / output rows staged
  * through LDS for 16-byte stores. */
+/* MFMA A operands of the Q.K product from the fp32 Q rows in LDS (1040-byte
+ * stride, q8_kdim order): rows 0-7 fp16(q), rows 8-15 the residual
+ * (nsel = -1); rows past gqa are zero. qbias[b] = qa[b] x (-1152) is the
+ * accumulator input that removes the +1152 bias of the K operands. */
+__device__ static inline void build_qa(const float *qraw, uint32_t g, uint32_t gqa, uint32_t jg,
+                                       float nsel, h8_t (&qa)[8], f4_t (&qbias)[8]) {
+    const float *qr = qraw + (g < gqa ? g : 0u) * 260u;
+    const float qs = g < gqa ? 1.f : 0.f;
+#pragma unroll
+    for (uint32_t b = 0; b < 8u; b++)
+#pragma unroll
+        for (uint32_t kk = 0; kk < 4u; kk++) {
+            const fv2 v = *(const fv2 *)(qr + 32u * b + q8_kdim(b, jg, 2u * kk));
+            qa[b][2u * kk] = split_sel(v[0] * qs, nsel);
+            qa[b][2u * kk + 1u] = split_sel(v[1] * qs, nsel);
+        }
+    const h8_t neg = (h8_t)((_Float16)-1152.0f);
+#pragma unroll
+    for (uint32_t b = 0; b < 8u; b++)
+        qbias[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[b], neg, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                          0);
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     constexpr uint32_t CP = 64, ROWB = 272, NCH = 17, NLD = 5;
@@ -802,19 +825,27 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     jcur[NLD] = c0 * CP + (tid & (CP - 1u));
 #pragma unroll
     for (uint32_t u = 0; u <= NLD; u++) raw[u] = -1;
-    if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
 
-    /* Q: one 1 KiB DMA per head row (coalesced), operands built after the
-     * first chunk's barrier */
+    /* Q: one 1 KiB DMA per head row (coalesced). Without the prep (every mode
+     * but MODE_PSTEP) and with 16-byte aligned rows, each wave DMAs every row
+     * itself (the waves write identical bytes), ahead of the index loads: the
+     * wait for those covers its own DMAs, so the wave builds its operands
+     * while the first chunk's rows are in flight, with no barrier. Otherwise
+     * the waves share the rows and build after the first chunk's barrier. */
     const uint32_t g = mrow & 7u;
     constexpr uint32_t QHS = MODE == MODE_PSTEP ? 512u : 256u; /* q head stride */
-    if ((((uintptr_t)it.q) & 15u) == 0) {
+    const bool q_own = MODE != MODE_PSTEP && (((uintptr_t)it.q) & 15u) == 0;
+    if (q_own) {
+        for (uint32_t h = 0; h < gqa; h++)
+            dma16(it.q + (size_t)h * QHS + 4u * lane, qraw + h * 260u);
+    } else if ((((uintptr_t)it.q) & 15u) == 0) {
         for (uint32_t h = wave; h < gqa; h += 4u)
             dma16(it.q + (size_t)h * QHS + 4u * lane, qraw + h * 260u);
     } else {
         for (uint32_t e = tid; e < gqa * 256u; e += 256u)
             qraw[(e >> 8) * 260u + (e & 255u)] = ldg(it.q + (e >> 8) * QHS + (e & 255u));
     }
+    if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
     if (MODE == MODE_PSTEP && s == 0u && it.gate) {
         /* the gate halves of the [q | gate] rows go to the gate buffer the
          * merge reads */
@@ -869,6 +900,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 *(uint16_t *)(vraw + r * ROWB + q * 2u) = ldg((const uint16_t *)(vbase + off));
             }
         }
+        if (q_own && c == c0) build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
         TRACE(2);
         __builtin_amdgcn_s_waitcnt(0);
         if (IS_STEP(MODE)) {
@@ -888,7 +920,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             __syncthreads();
         }
         TRACE(3);
-        if (c == c0) {
+        if (!q_own && c == c0) {
             if (MODE == MODE_PSTEP) {
                 /* query heads wave, wave + 4: RMSNorm + RoPE in place */
                 for (uint32_t h = wave; h < gqa; h += 4u)
@@ -896,21 +928,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                                   (int32_t)it.pos_new, a.rope_base, a.eps, lane);
                 __syncthreads();
             }
-            const float *qr = qraw + (g < gqa ? g : 0u) * 260u;
-            const float qs = g < gqa ? 1.f : 0.f;
-#pragma unroll
-            for (uint32_t b = 0; b < 8u; b++)
-#pragma unroll
-                for (uint32_t kk = 0; kk < 4u; kk++) {
-                    const fv2 v = *(const fv2 *)(qr + 32u * b + q8_kdim(b, jg, 2u * kk));
-                    qa[b][2u * kk] = split_sel(v[0] * qs, nsel);
-                    qa[b][2u * kk + 1u] = split_sel(v[1] * qs, nsel);
-                }
-            const h8_t neg = (h8_t)((_Float16)-1152.0f);
-#pragma unroll
-            for (uint32_t b = 0; b < 8u; b++)
-                qbias[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[b], neg,
-                                                                  (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
         }
         if (c + 1u < c1) {
 #pragma unroll
