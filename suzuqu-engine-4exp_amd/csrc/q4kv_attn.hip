@@ -845,6 +845,9 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         for (uint32_t e = tid; e < gqa * 256u; e += 256u)
             qraw[(e >> 8) * 260u + (e & 255u)] = ldg(it.q + (e >> 8) * QHS + (e & 255u));
     }
+    /* the index loads stay behind the Q DMAs, so the wait for them covers
+     * those too */
+    asm volatile("" ::: "memory");
     if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
     if (MODE == MODE_PSTEP && s == 0u && it.gate) {
         /* the gate halves of the [q | gate] rows go to the gate buffer the
@@ -900,7 +903,11 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 *(uint16_t *)(vraw + r * ROWB + q * 2u) = ldg((const uint16_t *)(vbase + off));
             }
         }
-        if (q_own && c == c0) build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+        if (q_own && c == c0) {
+            /* dense items load no indices: wait for the Q DMAs explicitly */
+            if (MODE == MODE_DENSE) __builtin_amdgcn_s_waitcnt(0);
+            build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+        }
         TRACE(2);
         __builtin_amdgcn_s_waitcnt(0);
         if (IS_STEP(MODE)) {
