@@ -1,0 +1,128 @@
+"""QSA attention on the GPU against closed forms that need no oracle run:
+
+- one valid position in a padded list: softmax weight 1, so the output is that
+  position's dequantised V row (times sigmoid(gate) when a gate is given);
+- identical keys: all scores equal, so the output is the mean of the listed
+  V rows;
+- the split-KV division does not change the result: one item alone (many
+  splits) and the same item inside a 24-item batch (fewer splits each) agree.
+
+Sizes follow config 1 (q8_0, hd 256, 16 Q / 2 KV heads, 2051-entry lists)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import q4kv
+from gpu_util import note, quantize_on_gpu
+from synth import WIDTH, heads, selection
+
+pytestmark = pytest.mark.gpu
+
+N_HEAD, N_KVH, HD = 16, 2, 256
+GQA = N_HEAD // N_KVH
+
+
+def _decode_idx_kv(rt, q, kc, vc, idx, width, max_kv, gate=None):
+    """q4_hip_qsa_decode_idx_kv for one token, per-KV-head lists [n_kvh][width]."""
+    dq, di = rt.upload(q), rt.upload(idx)
+    dg = rt.upload(gate) if gate is not None else None
+    do = rt.alloc(q.nbytes)
+    rt.h2d(do, np.full(q.size, np.nan, np.float32))
+    assert rt.lib.q4_hip_qsa_decode_idx_kv(dq, kc, vc, dg, do, di, width, N_KVH * width, width,
+                                           N_HEAD, N_KVH, HD, 1, max_kv, 1.0 / 16, q4kv.KV_Q8)
+    rt.sync()
+    out = rt.download(do, q.nbytes, np.float32).reshape(q.shape)
+    for p in (dq, di, dg, do):
+        if p:
+            rt.free(p)
+    return out
+
+
+def _dequant_rows(oracle, xb, ctx):
+    """[ctx][n_kvh][hd] fp32 values of a q8_0 cache image."""
+    return oracle.dequant_q8(xb, ctx * N_KVH * HD).reshape(ctx, N_KVH, HD).astype(np.float64)
+
+
+def test_single_valid_position_returns_its_v_row(rt, oracle):
+    rng = np.random.default_rng(900)
+    ctx = 5000
+    k, v = heads(rng, (ctx, N_KVH)), heads(rng, (ctx, N_KVH))
+    kc, _ = quantize_on_gpu(rt, k, q4kv.KV_Q8)
+    vc, _ = quantize_on_gpu(rt, v, q4kv.KV_Q8)
+    vd = _dequant_rows(oracle, oracle.quant_q8(v), ctx)
+    # the valid entry sits first, at a 64-entry chunk boundary, mid-chunk
+    # and last; every other entry is padding (-1) or out of range (>= max_kv)
+    for slot in (0, 63, 64, 1000, WIDTH - 1):
+        note(f"single valid entry at slot {slot}")
+        idx = np.full((N_KVH, WIDTH), -1, np.int32)
+        idx[:, 1::7] = ctx + 5  # out of range: skipped like padding
+        pos = rng.integers(0, ctx, N_KVH)
+        idx[:, slot] = pos
+        q = heads(rng, (1, N_HEAD))
+        got = _decode_idx_kv(rt, q, kc, vc, idx.ravel(), WIDTH, ctx)
+        for h in range(N_HEAD):
+            want = vd[pos[h // GQA], h // GQA]
+            np.testing.assert_allclose(got[0, h], want, rtol=1e-6, atol=1e-6,
+                                       err_msg=f"slot {slot} head {h}")
+        gate = rng.standard_normal((1, N_HEAD, HD)).astype(np.float32)
+        got = _decode_idx_kv(rt, q, kc, vc, idx.ravel(), WIDTH, ctx, gate=gate)
+        for h in range(N_HEAD):
+            sig = 1.0 / (1.0 + np.exp(-gate[0, h].astype(np.float64)))
+            want = vd[pos[h // GQA], h // GQA] * sig
+            np.testing.assert_allclose(got[0, h], want, rtol=1e-5, atol=1e-6,
+                                       err_msg=f"gated, slot {slot} head {h}")
+
+
+def test_identical_keys_give_the_mean_of_v(rt, oracle):
+    note("identical keys: mean of the listed V rows")
+    rng = np.random.default_rng(901)
+    ctx = 262144
+    # every position holds the same key row per KV head: equal scores
+    k = np.broadcast_to(heads(rng, (1, N_KVH)), (ctx, N_KVH, HD)).copy()
+    v = heads(rng, (ctx, N_KVH))
+    kc, _ = quantize_on_gpu(rt, k, q4kv.KV_Q8)
+    vc, _ = quantize_on_gpu(rt, v, q4kv.KV_Q8)
+    vd = _dequant_rows(oracle, oracle.quant_q8(v), ctx)
+    idx = np.stack([selection(rng, ctx - 1) for _ in range(N_KVH)]).astype(np.int32)
+    q = heads(rng, (1, N_HEAD))
+    got = _decode_idx_kv(rt, q, kc, vc, idx.ravel(), WIDTH, ctx)
+    for kh in range(N_KVH):
+        want = vd[idx[kh], kh].mean(axis=0)
+        for g in range(GQA):
+            np.testing.assert_allclose(got[0, kh * GQA + g], want, rtol=1e-4, atol=2e-5,
+                                       err_msg=f"kv head {kh} q head {g}")
+
+
+def test_result_does_not_depend_on_the_split_count(rt, oracle):
+    note("split-count independence: one item alone vs inside a 24-item batch")
+    rng = np.random.default_rng(902)
+    ctx, items = 262144, 12
+    k, v = heads(rng, (ctx, N_KVH)), heads(rng, (ctx, N_KVH))
+    kc, _ = quantize_on_gpu(rt, k, q4kv.KV_Q8)
+    vc, _ = quantize_on_gpu(rt, v, q4kv.KV_Q8)
+    q = heads(rng, (items, N_HEAD))
+    sel = np.stack([np.stack([selection(rng, ctx - 1 - 97 * i) for _ in range(N_KVH)])
+                    for i in range(items)]).astype(np.int32)
+    dq, dsel = rt.upload(q), rt.upload(sel)
+    dout = rt.alloc(q.nbytes)
+    rt.h2d(dout, np.full(q.size, np.nan, np.float32))
+    descs = (q4kv.SeqDesc * items)()
+    qb, ib = N_HEAD * HD * 4, N_KVH * WIDTH * 4
+    for i in range(items):
+        descs[i] = q4kv.SeqDesc(kc, vc, dq + i * qb, None, dout + i * qb, dsel + i * ib,
+                                WIDTH, WIDTH, ctx, 0)
+    dd = rt.alloc(ctypes.sizeof(descs))
+    assert rt.lib.q4_hip_h2d(dd, ctypes.addressof(descs), ctypes.sizeof(descs))
+    assert rt.lib.q4_hip_qsa_decode_batch(dd, items, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8,
+                                          WIDTH)
+    rt.sync()
+    batched = rt.download(dout, q.nbytes, np.float32).reshape(q.shape)
+    for i in range(items):
+        alone = _decode_idx_kv(rt, q[i:i + 1], kc, vc, sel[i].ravel(), WIDTH, ctx)
+        # the splits see different running maxima, so the exp2 weights, their
+        # hi/lo split and the merge round differently. The two results differ
+        # by up to ~2e-5 (each is within ~1e-4 of fp64); a merge error would
+        # show at the 1e-3 level or above
+        np.testing.assert_allclose(alone[0], batched[i], rtol=1e-4, atol=1e-4,
+                                   err_msg=f"item {i}")
