@@ -98,31 +98,55 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
     it.wnq = it.wnk = nullptr;
     it.pos_new = ~0u;
     if (IS_BATCH(MODE)) {
-        const q4kv_seq_desc *d =
-            (const q4kv_seq_desc *)((const uint8_t *)a.seqs + (size_t)t * a.desc_stride);
-        const float *gate = ldg(&d->gate);
-        const int32_t *idx = ldg(&d->idx);
-        const uint32_t n_sel = ldg(&d->n_sel);
-        it.kc = (const uint8_t *)ldg(&d->kcache);
-        it.vc = (const uint8_t *)ldg(&d->vcache);
-        it.q = ldg(&d->q) + hoff * (MODE == MODE_PSTEP ? 2u : 1u);
+        /* every descriptor word this mode reads, in one batch of scalar loads
+         * issued together (field-by-field loads behind the pointer tests
+         * cost extra dependent round trips before the first index load) */
+        constexpr uint32_t NW = MODE == MODE_PSTEP ? 28u : IS_STEP(MODE) ? 21u : 15u;
+        const uint32_t *dw =
+            (const uint32_t *)((const uint8_t *)a.seqs + (size_t)t * a.desc_stride);
+        uint32_t w[NW];
+#pragma unroll
+        for (uint32_t i = 0; i < NW; i++) w[i] = ldg(dw + i);
+        /* consume every word here so none of the loads sinks to its use */
+#pragma unroll
+        for (uint32_t i = 0; i < NW; i++) asm volatile("" ::"s"(w[i]));
+        auto ptr = [&](uint32_t byte_off) {
+            return (uintptr_t)w[byte_off / 4u] | ((uintptr_t)w[byte_off / 4u + 1u] << 32);
+        };
+        static_assert(offsetof(q4kv_seq_desc, kcache) == 0 && offsetof(q4kv_seq_desc, vcache) == 8 &&
+                          offsetof(q4kv_seq_desc, q) == 16 && offsetof(q4kv_seq_desc, gate) == 24 &&
+                          offsetof(q4kv_seq_desc, out) == 32 && offsetof(q4kv_seq_desc, idx) == 40 &&
+                          offsetof(q4kv_seq_desc, n_sel) == 48 &&
+                          offsetof(q4kv_seq_desc, idx_kvh_stride) == 52 &&
+                          offsetof(q4kv_seq_desc, max_kv) == 56,
+                      "q4kv_seq_desc layout");
+        static_assert(offsetof(q4kv_step_desc, k) == 64 && offsetof(q4kv_step_desc, v) == 72 &&
+                          offsetof(q4kv_step_desc, pos) == 80,
+                      "q4kv_step_desc layout");
+        static_assert(offsetof(q4kv_prep_step_desc, wn_q) == 96 &&
+                          offsetof(q4kv_prep_step_desc, wn_k) == 104,
+                      "q4kv_prep_step_desc layout");
+        const float *gate = (const float *)ptr(24);
+        const int32_t *idx = (const int32_t *)ptr(40);
+        const uint32_t n_sel = w[12];
+        it.kc = (const uint8_t *)ptr(0);
+        it.vc = (const uint8_t *)ptr(8);
+        it.q = (const float *)ptr(16) + hoff * (MODE == MODE_PSTEP ? 2u : 1u);
         it.gate = gate ? gate + hoff : nullptr;
-        it.out = ldg(&d->out) + hoff;
-        it.max_kv = ldg(&d->max_kv);
-        it.list = idx ? idx + (size_t)kh * ldg(&d->idx_kvh_stride) : nullptr;
+        it.out = (float *)ptr(32) + hoff;
+        it.max_kv = w[14];
+        it.list = idx ? idx + (size_t)kh * w[13] : nullptr;
         it.n = idx ? n_sel : (n_sel < it.max_kv ? n_sel : it.max_kv);
         it.lsrc = idx ? it.list : (const int32_t *)a.seqs;
         it.lmask = idx ? ~0u : 0u;
         if (IS_STEP(MODE)) {
-            const q4kv_step_desc *sd = (const q4kv_step_desc *)d;
-            it.knew = ldg(&sd->k) + (size_t)kh * a.hd;
-            it.vnew = ldg(&sd->v) + (size_t)kh * a.hd;
-            it.pos_new = ldg(&sd->pos);
+            it.knew = (const float *)ptr(64) + (size_t)kh * a.hd;
+            it.vnew = (const float *)ptr(72) + (size_t)kh * a.hd;
+            it.pos_new = w[20];
         }
         if (MODE == MODE_PSTEP) {
-            const q4kv_prep_step_desc *pd = (const q4kv_prep_step_desc *)d;
-            it.wnq = ldg(&pd->wn_q);
-            it.wnk = ldg(&pd->wn_k);
+            it.wnq = (const float *)ptr(96);
+            it.wnk = (const float *)ptr(104);
         }
     } else {
         const size_t qo = (size_t)t * a.n_head * a.hd + hoff;
