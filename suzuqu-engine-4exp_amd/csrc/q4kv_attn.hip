@@ -110,9 +110,11 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
         /* consume every word here so none of the loads sinks to its use */
 #pragma unroll
         for (uint32_t i = 0; i < NW; i++) asm volatile("" ::"s"(w[i]));
-        auto ptr = [&](uint32_t byte_off) {
+        auto word = [&](uint32_t byte_off) {
             return (uintptr_t)w[byte_off / 4u] | ((uintptr_t)w[byte_off / 4u + 1u] << 32);
         };
+        /* descriptor pointers as global-address-space pointers: accesses
+         * through them need no flat instructions */
         static_assert(offsetof(q4kv_seq_desc, kcache) == 0 && offsetof(q4kv_seq_desc, vcache) == 8 &&
                           offsetof(q4kv_seq_desc, q) == 16 && offsetof(q4kv_seq_desc, gate) == 24 &&
                           offsetof(q4kv_seq_desc, out) == 32 && offsetof(q4kv_seq_desc, idx) == 40 &&
@@ -126,27 +128,27 @@ __device__ static inline Item resolve_item(const AttnArgs &a, uint32_t item) {
         static_assert(offsetof(q4kv_prep_step_desc, wn_q) == 96 &&
                           offsetof(q4kv_prep_step_desc, wn_k) == 104,
                       "q4kv_prep_step_desc layout");
-        const float *gate = (const float *)ptr(24);
-        const int32_t *idx = (const int32_t *)ptr(40);
+        const float *gate = q4kv_gptr<const float>(word(24));
+        const int32_t *idx = q4kv_gptr<const int32_t>(word(40));
         const uint32_t n_sel = w[12];
-        it.kc = (const uint8_t *)ptr(0);
-        it.vc = (const uint8_t *)ptr(8);
-        it.q = (const float *)ptr(16) + hoff * (MODE == MODE_PSTEP ? 2u : 1u);
+        it.kc = q4kv_gptr<const uint8_t>(word(0));
+        it.vc = q4kv_gptr<const uint8_t>(word(8));
+        it.q = q4kv_gptr<const float>(word(16)) + hoff * (MODE == MODE_PSTEP ? 2u : 1u);
         it.gate = gate ? gate + hoff : nullptr;
-        it.out = (float *)ptr(32) + hoff;
+        it.out = q4kv_gptr<float>(word(32)) + hoff;
         it.max_kv = w[14];
         it.list = idx ? idx + (size_t)kh * w[13] : nullptr;
         it.n = idx ? n_sel : (n_sel < it.max_kv ? n_sel : it.max_kv);
         it.lsrc = idx ? it.list : (const int32_t *)a.seqs;
         it.lmask = idx ? ~0u : 0u;
         if (IS_STEP(MODE)) {
-            it.knew = (const float *)ptr(64) + (size_t)kh * a.hd;
-            it.vnew = (const float *)ptr(72) + (size_t)kh * a.hd;
+            it.knew = q4kv_gptr<const float>(word(64)) + (size_t)kh * a.hd;
+            it.vnew = q4kv_gptr<const float>(word(72)) + (size_t)kh * a.hd;
             it.pos_new = w[20];
         }
         if (MODE == MODE_PSTEP) {
-            it.wnq = (const float *)ptr(96);
-            it.wnk = (const float *)ptr(104);
+            it.wnq = q4kv_gptr<const float>(word(96));
+            it.wnk = q4kv_gptr<const float>(word(104));
         }
     } else {
         const size_t qo = (size_t)t * a.n_head * a.hd + hoff;
@@ -1284,7 +1286,7 @@ __global__ __launch_bounds__(256) void qsa_comb_gemv_k(AttnArgs a, const q4kv_ou
     }
     __syncthreads();
     const uint8_t *w = (const uint8_t *)ldg(&od[seq].w_o);
-    float *y = ldg(&od[seq].y);
+    float *y = q4kv_gptr_at(&od[seq].y);
     const size_t rowb = (size_t)(a.n_head * hd / 32u) * 34u;
     const uint32_t pr = lane & 3u; /* this lane's block pair (64 columns) */
     const uint32_t rend = min(n_embd, (rb + 1u) * OUT_RPB);

@@ -45,10 +45,19 @@ namespace {
 
 constexpr uint32_t IDX_HD = 128;
 
-/* Vector loads/stores (HIP's vector classes do not take an address-space
- * qualified copy; these pointers are global kernel arguments). */
-template <class T> __device__ inline T ld_vec(const T *p) { return *p; }
-template <class T> __device__ inline void st_vec(T *p, T v) { *p = v; }
+/* Global-memory vector loads/stores (HIP's vector classes do not take an
+ * address-space qualified copy, so they go through native vector types). */
+typedef float idx_f2 __attribute__((ext_vector_type(2)));
+typedef float idx_f4 __attribute__((ext_vector_type(4)));
+__device__ inline float4 ld_vec(const float4 *p) {
+    const idx_f4 v = *(const GLOBAL idx_f4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ inline float2 ld_vec(const float2 *p) {
+    const idx_f2 v = *(const GLOBAL idx_f2 *)p;
+    return make_float2(v.x, v.y);
+}
+__device__ inline void st_vec(float2 *p, float2 v) { *(GLOBAL idx_f2 *)p = (idx_f2){v.x, v.y}; }
 
 /* the shared wave arithmetic of q4kv_internal.h under short names */
 __device__ inline float sum8(float v) { return q4kv_sum8(v); }
@@ -144,29 +153,43 @@ constexpr uint32_t SC_ROWS_WG = 64; /* 4 waves x 2 x 8 rows */
  * eight lanes per row, lane g holding dims {32i + 4g .. +3 : i < 4} of each
  * query in qr. Row b_new, when in range, is taken from nr (this lane's dims
  * of the pooled row this launch produced) instead of the pool. */
-__device__ __attribute__((always_inline)) inline void score_rows(const float4 (&qr)[4][4], const float *pool, float *srow,
-                                  uint32_t rb, uint32_t n_blocks, uint32_t n_vis,
-                                  uint32_t lane, uint32_t wave, float4 nr0, float4 nr1,
-                                  float4 nr2, float4 nr3, uint32_t b_new) {
+/* this lane's dims of its two rows of the 64-row group at rb (rows past
+ * n_vis re-read the last visible row) */
+__device__ __attribute__((always_inline)) inline void score_load(float4 (&p)[2][4], const float *pool,
+                                                                 uint32_t rb, uint32_t n_vis,
+                                                                 uint32_t lane, uint32_t wave) {
     const uint32_t g = lane & 7u, rsub = lane >> 3;
     const uint32_t rlast = n_vis ? n_vis - 1 : 0;
-    for (; rb < n_blocks; rb += gridDim.x * SC_ROWS_WG) {
-        float4 p[2][4];
-        uint32_t row[2];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            row[u] = rb + wave * 16u + 8u * u + rsub;
-            const uint32_t r = row[u] < rlast ? row[u] : rlast;
-            const float4 *src = (const float4 *)(pool + (size_t)r * IDX_HD) + g;
+    for (int u = 0; u < 2; u++) {
+        const uint32_t row = rb + wave * 16u + 8u * u + rsub;
+        const uint32_t r = row < rlast ? row : rlast;
+        const float4 *src = (const float4 *)(pool + (size_t)r * IDX_HD) + g;
 #pragma unroll
-            for (int i = 0; i < 4; i++) p[u][i] = ld_vec(src + 8 * i);
-            if (row[u] == b_new) {
-                p[u][0] = nr0;
-                p[u][1] = nr1;
-                p[u][2] = nr2;
-                p[u][3] = nr3;
-            }
+        for (int i = 0; i < 4; i++) p[u][i] = ld_vec(src + 8 * i);
+    }
+}
+
+/* Scores of the two rows score_load fetched (row b_new taken from nr). */
+__device__ __attribute__((always_inline)) inline void score_store(const float4 (&qr)[4][4], float4 (&p)[2][4],
+                                                                  float *srow, uint32_t rb,
+                                                                  uint32_t n_blocks, uint32_t n_vis,
+                                                                  uint32_t lane, uint32_t wave,
+                                                                  float4 nr0, float4 nr1, float4 nr2,
+                                                                  float4 nr3, uint32_t b_new) {
+    const uint32_t g = lane & 7u, rsub = lane >> 3;
+    uint32_t row[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        row[u] = rb + wave * 16u + 8u * u + rsub;
+        if (row[u] == b_new) {
+            p[u][0] = nr0;
+            p[u][1] = nr1;
+            p[u][2] = nr2;
+            p[u][3] = nr3;
         }
+    }
+    {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             float s = 0.f;
@@ -182,8 +205,19 @@ __device__ __attribute__((always_inline)) inline void score_rows(const float4 (&
                 }
                 s += fmaxf(sum8(d), 0.f);
             }
-            if (g == 0 && row[u] < n_blocks) srow[row[u]] = row[u] < n_vis ? s : -1.0e30f;
+            if (g == 0 && row[u] < n_blocks) stg(srow + row[u], row[u] < n_vis ? s : -1.0e30f);
         }
+    }
+}
+
+__device__ __attribute__((always_inline)) inline void score_rows(const float4 (&qr)[4][4], const float *pool, float *srow,
+                                  uint32_t rb, uint32_t n_blocks, uint32_t n_vis,
+                                  uint32_t lane, uint32_t wave, float4 nr0, float4 nr1,
+                                  float4 nr2, float4 nr3, uint32_t b_new) {
+    for (; rb < n_blocks; rb += gridDim.x * SC_ROWS_WG) {
+        float4 p[2][4];
+        score_load(p, pool, rb, n_vis, lane, wave);
+        score_store(qr, p, srow, rb, n_blocks, n_vis, lane, wave, nr0, nr1, nr2, nr3, b_new);
     }
 }
 
@@ -244,13 +278,13 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
     uint32_t pos;
     if (BATCH) { /* item blockIdx.y of a batch: its own buffers and position */
         const q4kv_index_desc *d = descs + blockIdx.y;
-        raw2 = (uint32_t *)ldg(&d->raw);
-        pool = ldg(&d->pool);
-        wn_k = ldg(&d->wn_k);
-        k_new = ldg(&d->k_new);
-        q = ldg(&d->q);
-        wn_q = ldg(&d->wn_q);
-        score = ldg(&d->score);
+        raw2 = q4kv_gptr<uint32_t>(ldg((const uintptr_t *)&d->raw));
+        pool = q4kv_gptr_at(&d->pool);
+        wn_k = q4kv_gptr_at(&d->wn_k);
+        k_new = q4kv_gptr_at(&d->k_new);
+        q = q4kv_gptr_at(&d->q);
+        wn_q = q4kv_gptr_at(&d->wn_q);
+        score = q4kv_gptr_at(&d->score);
         pos = ldg(&d->pos);
     } else {
         pos = (uint32_t)*pp;
@@ -258,22 +292,32 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
     const uint32_t n_vis = (pos + 1) / ratio;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t rb = blockIdx.x * SC_ROWS_WG;
-    /* fp16 pair of the new key this lane owns (dims 2*lane, 2*lane+1) */
+    /* the small loads first (the new key pair this lane owns, dims 2*lane and
+     * 2*lane+1; its query pair; its RMSNorm weights), branch-free, then this
+     * workgroup's first 64 rows: the query preparation below waits only for
+     * the small ones and overlaps the rows (row b_new, pooled below, is
+     * replaced before use); rows past the grid follow in grid strides */
     const float2 kn = ld_vec((const float2 *)k_new + lane);
+    float2 x = ld_vec((const float2 *)(q + (wave < n_head ? wave : 0u) * IDX_HD) + lane);
+    float2 w = ld_vec((const float2 *)(wn_q ? wn_q : k_new) + lane);
+    const bool live = rb < n_vis;
+    float4 p[2][4];
+    asm volatile("" ::: "memory");
+    score_load(p, pool, rb, n_vis, lane, wave); /* no branch: workgroups past n_vis
+                                                     * re-read the last row, unused */
     const uint32_t kh = (uint32_t)__half_as_ushort(__float2half_rn(kn.x)) |
                         ((uint32_t)__half_as_ushort(__float2half_rn(kn.y)) << 16);
     if (blockIdx.x == 0 && wave == 0) stg(raw2 + (size_t)pos * (IDX_HD / 2) + lane, kh);
-    if (rb >= n_vis) return;
+    if (!live) return;
     const float freq = 2 * lane < n_rot ? rope_freq(base, lane, n_rot / 2) : 0.f;
     /* indexer queries: wave h prepares head h (qsa_prep_k's arithmetic) */
     {
-        float2 x = make_float2(0.f, 0.f);
-        if (wave < n_head) x = ld_vec((const float2 *)(q + wave * IDX_HD) + lane);
+        if (wave >= n_head) x = make_float2(0.f, 0.f);
+        if (!wn_q) w = make_float2(1.f, 1.f);
         float ss = fmaf(x.x, x.x, 0.f);
         ss = fmaf(x.y, x.y, ss);
         ss = wave_sum(ss);
         const float scale = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)IDX_HD) + eps));
-        const float2 w = wn_q ? ld_vec((const float2 *)wn_q + lane) : make_float2(1.f, 1.f);
         float y0 = x.x * scale * w.x, y1 = x.y * scale * w.y;
         if (2 * lane < n_rot) rope_rotate(y0, y1, (float)pos, freq);
         if (wave >= n_head) y0 = y1 = 0.f;
@@ -282,7 +326,8 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
     }
     const bool completes = (pos + 1) % ratio == 0;
     const uint32_t b_new = completes ? n_vis - 1 : 0xffffffffu;
-    if (completes && b_new >= rb && b_new < rb + SC_ROWS_WG && wave == 0) {
+    /* the workgroup whose grid-stride row groups hold b_new pools it */
+    if (completes && (b_new / SC_ROWS_WG) % gridDim.x == blockIdx.x && wave == 0) {
         const float2 v = pool_block(raw2, pool, wn_k, ratio, b_new, n_rot, freq, eps, lane,
                                     true, kh);
         new_row[2 * lane] = v.x;
@@ -297,7 +342,9 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
         for (int i = 0; i < 4; i++) qr[h][i] = *(const float4 *)&qs[h][32 * i + 4 * g];
 #pragma unroll
     for (int i = 0; i < 4; i++) nr[i] = *(const float4 *)&new_row[32 * i + 4 * g];
-    score_rows(qr, pool, score, rb, n_vis, n_vis, lane, wave, nr[0], nr[1], nr[2], nr[3], b_new);
+    score_store(qr, p, score, rb, n_vis, n_vis, lane, wave, nr[0], nr[1], nr[2], nr[3], b_new);
+    score_rows(qr, pool, score, rb + gridDim.x * SC_ROWS_WG, n_vis, n_vis, lane, wave, nr[0],
+               nr[1], nr[2], nr[3], b_new);
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -543,8 +590,8 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
     if (SRC == TK_BATCH) {
         const q4kv_index_desc *d = descs + t;
         pos = ldg(&d->pos);
-        row = ldg(&d->score);
-        out = ldg(&d->sel);
+        row = q4kv_gptr_at(&d->score);
+        out = q4kv_gptr_at(&d->sel);
     } else {
         pos = (SRC == TK_DEV ? (uint32_t)*pp : pos0) + t;
         row = score + (size_t)t * stride;
@@ -553,7 +600,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
     const uint32_t n_vis = (pos + 1) / ratio;
     const uint32_t need = n_vis < k_blk ? n_vis : k_blk;
     if (need == n_vis) { /* every complete block fits: the dense prefix */
-        for (uint32_t w = tid; w < width; w += TK_T) out[w] = w <= pos ? (int32_t)w : -1;
+        for (uint32_t w = tid; w < width; w += TK_T) stg(out + w, w <= pos ? (int32_t)w : -1);
         return;
     }
     constexpr uint32_t TK_CHUNK = TK_T * KPT;
@@ -832,7 +879,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
             const uint32_t tail = n_vis * ratio + (w - ncs);
             v = tail <= pos ? (int32_t)tail : -1;
         }
-        out[w] = v;
+        stg(out + w, v);
     }
 }
 

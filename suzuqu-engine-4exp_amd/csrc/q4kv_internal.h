@@ -33,6 +33,15 @@ bool q4kv_append_steps(const void *d_step_descs, uint32_t n_desc, uint32_t n, ui
  * accesses, whose waits also cover LDS traffic. */
 template <class T> __device__ static inline T ldg(const T *p) { return *(const GLOBAL T *)p; }
 template <class T> __device__ static inline void stg(T *p, T v) { *(GLOBAL T *)p = v; }
+/* A pointer read from device memory (a descriptor field) is a generic
+ * pointer: accesses through it compile to flat memory instructions, which
+ * also count against lgkmcnt. Built from the field's integer value as a
+ * global-address-space pointer instead, it lets the compiler use global
+ * instructions for every access through it. */
+template <class T> __device__ static inline T *q4kv_gptr(uintptr_t v) { return (T *)(GLOBAL T *)v; }
+template <class T> __device__ static inline T *q4kv_gptr_at(T *const *field) {
+    return q4kv_gptr<T>(ldg((const uintptr_t *)field));
+}
 
 /* One lane's share of a q8_0 block (src/q4_rocm.cu:7221-7238): lanes 8k ..
  * 8k+7 of a wave hold the block's 32 values, four each (lane part p holds
@@ -108,7 +117,7 @@ constexpr uint32_t Q4KV_PREP_MAXP = 8; /* pairs per lane: hd <= 1024 */
  * Lane l owns pairs p = l + 64m; in and out may alias (every lane reads its
  * pairs before the reduction). Every kernel that prepares rows calls this,
  * so their results agree bit for bit. */
-__device__ static inline void q4kv_prep_row(const float *in, float *out, const float *wn,
+__device__ static inline __attribute__((always_inline)) void q4kv_prep_row(const float *in, float *out, const float *wn,
                                             uint32_t hd, uint32_t n_rot, int32_t pos,
                                             float base, float eps, uint32_t lane) {
     const uint32_t np = hd / 2;
