@@ -787,16 +787,20 @@ __device__ static inline void build_qa(const float *qraw, uint32_t g, uint32_t g
                                                           0);
 }
 
-template <int MODE>
+/* DB: two row buffers, chunk c + 1's rows DMA'd while chunk c is computed
+ * (for workgroups with many chunks: prefill); the Q rows are staged in the
+ * second buffer, which the first chunk does not use. */
+template <int MODE, bool DB>
 __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     constexpr uint32_t CP = 64, ROWB = 272, NCH = 17, NLD = 5;
-    __shared__ __attribute__((aligned(16))) uint8_t kraw[CP * ROWB];
-    __shared__ __attribute__((aligned(16))) uint8_t vraw[CP * ROWB];
+    /* row buffers: [K rows | V rows] each */
+    __shared__ __attribute__((aligned(16))) uint8_t rowbuf[DB ? 2 : 1][2 * CP * ROWB];
     __shared__ __attribute__((aligned(16))) float sw[8 * CP];  /* weights [head][pos] */
     __shared__ __attribute__((aligned(16))) float vsc[8 * CP]; /* V scales [block][pos] */
     /* raw fp32 Q rows, 1040-byte stride (4 pad floats) against bank conflicts */
-    __shared__ __attribute__((aligned(16))) float qraw[8 * 260];
-    __shared__ int32_t s_pos[CP];
+    __shared__ __attribute__((aligned(16))) float qraw_s[DB ? 1 : 8 * 260];
+    float *const qraw = DB ? (float *)rowbuf[DB ? 1 : 0] : qraw_s;
+    __shared__ int32_t s_pos[DB ? 2 : 1][CP];
     __shared__ float s_cmax[4][8], s_psum[4][8], s_ml[2][8];
     __shared__ __attribute__((aligned(16))) float kst[MODE == MODE_PSTEP ? 256 : 1];
 
@@ -905,9 +909,12 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         acc[i] = (f4_t){0.f, 0.f, 0.f, 0.f};
     }
 
-    for (uint32_t c = c0; c < c1; c++) {
+    /* positions of chunk c (from the index loads in flight) into s_pos[bs],
+     * and its K and V rows into buffer bs */
+    auto issue_rows = [&](uint32_t c, uint32_t bs) {
         pos_finish<NLD + 1, MODE>(it, jcur, raw, pidx);
-        if (tid < CP) s_pos[tid] = pidx[NLD];
+        if (tid < CP) s_pos[bs][tid] = pidx[NLD];
+        uint8_t *kr = rowbuf[bs], *vr = rowbuf[bs] + CP * ROWB;
         if (al16) {
 #pragma unroll
             for (uint32_t u = 0; u < NLD; u++) {
@@ -916,8 +923,8 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                     const uint32_t r = e / NCH, q = e - r * NCH;
                     const size_t off = (size_t)(pidx[u] < 0 ? 0 : pidx[u]) * rstride + q * 16u;
                     (void)r;
-                    dma16(kbase + off, kraw + e0 * 16u);
-                    dma16(vbase + off, vraw + e0 * 16u);
+                    dma16(kbase + off, kr + e0 * 16u);
+                    dma16(vbase + off, vr + e0 * 16u);
                 }
             }
         } else {
@@ -925,16 +932,41 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 const uint32_t r = e / (ROWB / 2u), q = e - r * (ROWB / 2u);
                 const int32_t p = item_pos(it, c * CP + r);
                 const size_t off = (size_t)(p < 0 ? 0 : p) * rstride + q * 2u;
-                *(uint16_t *)(kraw + r * ROWB + q * 2u) = ldg((const uint16_t *)(kbase + off));
-                *(uint16_t *)(vraw + r * ROWB + q * 2u) = ldg((const uint16_t *)(vbase + off));
+                *(uint16_t *)(kr + r * ROWB + q * 2u) = ldg((const uint16_t *)(kbase + off));
+                *(uint16_t *)(vr + r * ROWB + q * 2u) = ldg((const uint16_t *)(vbase + off));
             }
         }
-        if (q_own && c == c0) {
-            /* dense items load no indices: wait for the Q DMAs explicitly */
-            if (MODE == MODE_DENSE) __builtin_amdgcn_s_waitcnt(0);
+    };
+    if (DB && c0 < c1) {
+        /* the first chunk's rows, then the second chunk's indices */
+        if (q_own && MODE == MODE_DENSE) {
+            __builtin_amdgcn_s_waitcnt(0);
             build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
         }
+        issue_rows(c0, 0u);
+        if (q_own && MODE != MODE_DENSE) build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+        if (c0 + 1u < c1) {
+#pragma unroll
+            for (uint32_t u = 0; u <= NLD; u++) jcur[u] += CP;
+            pos_issue<NLD + 1, MODE>(it, jcur, raw);
+        }
+    }
+
+    for (uint32_t c = c0; c < c1; c++) {
+        const uint32_t bs = DB ? (c - c0) & 1u : 0u;
+        if (!DB) {
+            /* one buffer: this chunk's rows now */
+            issue_rows(c, 0u);
+            if (q_own && c == c0) {
+                /* dense items load no indices: wait for the Q DMAs explicitly */
+                if (MODE == MODE_DENSE) __builtin_amdgcn_s_waitcnt(0);
+                build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+            }
+        }
+        uint8_t *const kraw = rowbuf[bs], *const vraw = rowbuf[bs] + CP * ROWB;
+        const int32_t *const spos = s_pos[bs];
         TRACE(2);
+        /* this chunk's rows (with DB, also the next chunk's indices) have landed */
         __builtin_amdgcn_s_waitcnt(0);
         if (IS_STEP(MODE)) {
             /* rows at the appended position take the new token's bytes */
@@ -945,7 +977,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                     const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
                     uint8_t *base = (tid < 64u ? kraw : vraw) + 34u * ((tid >> 3) & 7u);
                     for (uint32_t r = 0; r < CP; r++)
-                        if ((uint32_t)s_pos[r] == it.pos_new) q8_lane_store(base + r * ROWB, tid & 7u, d, q);
+                        if ((uint32_t)spos[r] == it.pos_new) q8_lane_store(base + r * ROWB, tid & 7u, d, q);
                 }
                 __syncthreads();
             }
@@ -962,18 +994,28 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 __syncthreads();
             }
             build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+            if (DB) __syncthreads(); /* buffer 1 (the Q rows) is refilled below */
         }
         if (c + 1u < c1) {
+            if (DB) {
+                issue_rows(c + 1u, bs ^ 1u);
+                if (c + 2u < c1) {
 #pragma unroll
-            for (uint32_t u = 0; u <= NLD; u++) jcur[u] += CP;
-            pos_issue<NLD + 1, MODE>(it, jcur, raw);
+                    for (uint32_t u = 0; u <= NLD; u++) jcur[u] += CP;
+                    pos_issue<NLD + 1, MODE>(it, jcur, raw);
+                }
+            } else {
+#pragma unroll
+                for (uint32_t u = 0; u <= NLD; u++) jcur[u] += CP;
+                pos_issue<NLD + 1, MODE>(it, jcur, raw);
+            }
         }
         /* V block scales, 0 for masked positions */
 #pragma unroll
         for (uint32_t k = 0; k < 2u; k++) {
             const uint32_t e = tid + 256u * k, b = e >> 6, r = e & 63u;
             const float x = ld_f16(vraw + r * ROWB + 34u * b);
-            vsc[e] = s_pos[r] < 0 ? 0.f : x;
+            vsc[e] = spos[r] < 0 ? 0.f : x;
         }
         /* ---- scores: wave w, positions 16w .. 16w+15 ---- */
         const uint32_t r = wave * 16u + mrow;
@@ -1002,7 +1044,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             S += ks * C;
         }
         TRACE(4);
-        const bool valid = s_pos[r] >= 0;
+        const bool valid = spos[r] >= 0;
         float T[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
@@ -1082,7 +1124,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     }
 
     /* ---- epilogue: hi+lo rows -> LDS [head][col], then 16-byte stores ---- */
-    float *so = (float *)kraw; /* 8 x 256 floats, free after the last chunk */
+    float *so = (float *)rowbuf[0]; /* 8 x 256 floats, free after the last chunk */
     if (c0 >= c1) __syncthreads();
 #pragma unroll
     for (uint32_t t = 0; t < 4u; t++)
@@ -1393,8 +1435,12 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         dim3 grid(S, ni);
         const bool prof = prof_armed();
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
-        if (fast)
-            qsa_q8d256_k<MODE><<<grid, 256, 0, q4kv_stream>>>(a);
+        /* double-buffered rows pay when a workgroup walks many chunks
+         * (prefill); with one or two (decode) the extra LDS traffic does not */
+        if (fast && !IS_STEP(MODE) && cps >= 3u)
+            qsa_q8d256_k<IS_STEP(MODE) ? MODE_BATCH : MODE, true><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (fast)
+            qsa_q8d256_k<MODE, false><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (IS_STEP(MODE))
             return false;
         else if (gqa <= 8u)
