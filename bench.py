@@ -771,7 +771,7 @@ def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
     """The indexer of config 3's chunked prefill (src/q4_fwd.c:740-770, sliced by 512
     tokens as src/q4_fwd.c:1744-1754): for each 512-token slice of an 8192-token
     chunk after a 16384-token cache, the indexer queries' RMSNorm + RoPE
-    (q4_hip_qsa_k_prep_n), the scores of every visible block (fp32 MFMA), and the
+    (q4_hip_qsa_k_prep_n), the scores of every visible block (bf16x3 split on MFMA), and the
     top-512 selection of every token expanded to 2051 positions. The pool of all
     6144 blocks is rebuilt first (q4_hip_qsa_pool), as a new chunk's keys arrive."""
     rt, lib = b.rt, b.lib
@@ -820,7 +820,7 @@ def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
         rt.free(p_)
     return {"what": f"indexer of an {chunk}-token prefill chunk after a {cache}-token cache, "
                     f"{slice_}-token slices: pool rebuild ({nb} blocks), query prep, scores "
-                    "(fp32 MFMA), top-512 + expansion per token",
+                    "(bf16x3 split on MFMA), top-512 + expansion per token",
             "us_per_layer": round(t * 1e6, 1), "us_per_token": round(t * 1e6 / chunk, 3),
             "score_gflop": round(flop / 1e9, 1)}
 
