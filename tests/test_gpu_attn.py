@@ -192,11 +192,13 @@ def test_shared_list_reference_entry_and_short_lists(rt, oracle):
     assert not got.any()
 
 
-@pytest.mark.parametrize("kind", [2, 1])
-def test_prefill_indexed_and_dense_causal(rt, oracle, kind):
-    note(f"prefill kind={kind}")
-    rng = np.random.default_rng(500 + kind)
-    n_head, n_kvh, hd, base, n_tok = 16, 2, 256, 2500, 96
+# 96 tokens (192 items, two splits each); 160 q8_0 tokens (320 items): one
+# split per item, 33 chunks per workgroup, the double-buffered instance
+@pytest.mark.parametrize("kind,n_tok", [(2, 96), (1, 96), (2, 160)])
+def test_prefill_indexed_and_dense_causal(rt, oracle, kind, n_tok):
+    note(f"prefill kind={kind} n_tok={n_tok}")
+    rng = np.random.default_rng(500 + kind + n_tok)
+    n_head, n_kvh, hd, base = 16, 2, 256, 2500
     ctx = base + n_tok
     k, v = heads(rng, (ctx, n_kvh)), heads(rng, (ctx, n_kvh))
     q = heads(rng, (n_tok, n_head))
