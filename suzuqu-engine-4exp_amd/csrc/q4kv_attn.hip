@@ -1435,10 +1435,11 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         dim3 grid(S, ni);
         const bool prof = prof_armed();
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
-        /* double-buffered rows pay when a workgroup walks many chunks
-         * (prefill); with one or two (decode) the extra LDS traffic does not */
-        if (fast && !IS_STEP(MODE) && cps >= 3u)
-            qsa_q8d256_k<IS_STEP(MODE) ? MODE_BATCH : MODE, true><<<grid, 256, 0, q4kv_stream>>>(a);
+        /* double-buffered rows pay when a workgroup walks three or more chunks
+         * (prefill, batched decode of many sequences); with one or two (the
+         * 12-layer step) the extra LDS traffic does not */
+        if (fast && cps >= 3u)
+            qsa_q8d256_k<MODE, true><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (fast)
             qsa_q8d256_k<MODE, false><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (IS_STEP(MODE))
