@@ -382,11 +382,14 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
                                                         uint32_t n_blocks, uint32_t stride,
                                                         uint32_t n_head, uint32_t pos0,
                                                         uint32_t ratio) {
+    /* the A operands (the workgroup's 16 tokens x 4 heads) are the same for
+     * its four waves: wave w loads and splits k-step w once, into LDS */
+    __shared__ s16x8 a_hi[4][4][64], a_lo[4][4][64]; /* [k-step][tile][lane] */
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t i16 = lane & 15u, kq = lane >> 4;
     const uint32_t tok0 = blockIdx.y * 16u;
     const uint32_t blk0 = blockIdx.x * 256u + wave * 64u;
-    if (blk0 >= n_blocks) return;
+    if (blockIdx.x * 256u >= n_blocks) return;
 
     const float *ap[4];
     bool av[4];
@@ -403,6 +406,15 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
         blk = blk < n_blocks ? blk : n_blocks - 1;
         bp[b] = pool + (size_t)blk * IDX_HD + 8u * kq;
     }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 x0 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * wave)) : z;
+        const float4 x1 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * wave) + 1) : z;
+        split_bf16(x0, x1, a_hi[wave][a][lane], a_lo[wave][a][lane]);
+    }
+    __syncthreads();
+    if (blk0 >= n_blocks) return;
     f32x4 acc[4][4];
 #pragma unroll
     for (int a = 0; a < 4; a++)
@@ -414,10 +426,8 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
         s16x8 Ah[4], Al[4], Bh[4], Bl[4];
 #pragma unroll
         for (int a = 0; a < 4; a++) {
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 x0 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * st)) : z;
-            const float4 x1 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * st) + 1) : z;
-            split_bf16(x0, x1, Ah[a], Al[a]);
+            Ah[a] = a_hi[st][a][lane];
+            Al[a] = a_lo[st][a][lane];
         }
 #pragma unroll
         for (int b = 0; b < 4; b++) {
