@@ -24,25 +24,13 @@ __global__ __launch_bounds__(256) void gemv_q8_k(const uint8_t *w, const float *
     __shared__ __attribute__((aligned(16))) float xs[GV_MAXCOLS];
     __shared__ float xsum[GV_MAXCOLS / 32];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    for (uint32_t i = tid; i < ncols / 4u; i += 256u)
-        ((float4 *)xs)[i] = ((const float4 *)x)[i];
-    __syncthreads();
     const uint32_t nb = ncols / 32u;
-    for (uint32_t b = tid; b < nb; b += 256u) {
-        float s = 0.f;
-        for (int i = 0; i < 32; i++) s += xs[32u * b + i];
-        xsum[b] = s;
-    }
-    __syncthreads();
     const uint32_t npair = ncols / 64u;
     const size_t rowb = (size_t)nb * 34u;
     const uint32_t r0 = (blockIdx.x * 4u + wave) * GV_RPW;
-    float acc[GV_RPW];
-#pragma unroll
-    for (uint32_t j = 0; j < GV_RPW; j++) acc[j] = 0.f;
-    for (uint32_t p = lane; p < npair; p += 64u) {
-        const float xa = xsum[2u * p], xb = xsum[2u * p + 1u];
-        uint32_t dw[GV_RPW][17];
+    /* 17 dwords (a block pair) of each of the wave's rows at pair p */
+    uint32_t dw[GV_RPW][17];
+    auto load_pair = [&](uint32_t p) {
 #pragma unroll
         for (uint32_t j = 0; j < GV_RPW; j++) {
             const uint32_t r = min(r0 + j, nrows - 1u);
@@ -50,6 +38,37 @@ __global__ __launch_bounds__(256) void gemv_q8_k(const uint8_t *w, const float *
 #pragma unroll
             for (int k = 0; k < 17; k++) dw[j][k] = ldg(src + k);
         }
+    };
+    /* x is loaded first, then the first pair's weights: x reaches LDS (its
+     * wait does not cover the weights, issued later) and the block sums are
+     * formed while the weights are in flight */
+    constexpr uint32_t XPT = GV_MAXCOLS / 4u / 256u; /* four-float groups of x per thread */
+    typedef float xf4 __attribute__((ext_vector_type(4)));
+    xf4 xv[XPT];
+#pragma unroll
+    for (uint32_t k = 0; k < XPT; k++) {
+        const uint32_t i = tid + 256u * k;
+        xv[k] = ldg((const xf4 *)x + (i < ncols / 4u ? i : 0u));
+    }
+    __builtin_amdgcn_sched_barrier(0); /* keep the x loads ahead of the weights */
+    load_pair(lane < npair ? lane : 0u);
+    /* every index is inside xs (XPT x 256 float4 = GV_MAXCOLS floats); the
+     * entries past ncols are not read */
+#pragma unroll
+    for (uint32_t k = 0; k < XPT; k++) ((xf4 *)xs)[tid + 256u * k] = xv[k];
+    __syncthreads();
+    for (uint32_t b = tid; b < nb; b += 256u) {
+        float s = 0.f;
+        for (int i = 0; i < 32; i++) s += xs[32u * b + i];
+        xsum[b] = s;
+    }
+    __syncthreads();
+    float acc[GV_RPW];
+#pragma unroll
+    for (uint32_t j = 0; j < GV_RPW; j++) acc[j] = 0.f;
+    for (uint32_t p = lane; p < npair; p += 64u) {
+        if (p != lane) load_pair(p);
+        const float xa = xsum[2u * p], xb = xsum[2u * p + 1u];
 #pragma unroll
         for (uint32_t j = 0; j < GV_RPW; j++) acc[j] += q4kv_q8_pair_dot(dw[j], xs, p, xa, xb);
     }
