@@ -469,6 +469,8 @@ def config4(b, steps=100, sets=4, layers=4):
     restore of a 100000-token x 12-layer q8_0 session image from pinned host
     memory."""
     rt, lib = b.rt, b.lib
+    # the descriptors address the Bench's per-(set, layer) rows and outputs
+    assert b.L >= layers and b.R >= sets, "config4 needs a Bench of >= 4 layers and sets"
     out = {}
     for kind, name in ((q4kv.KV_F16, "f16"), (q4kv.KV_F32, "f32")):
         bpt = q4kv.token_bytes(kind, N_KVH, HD)
@@ -546,6 +548,7 @@ def config_prep(b, steps=200, sets=4, rot=64, base=1.0e7, eps=1.0e-6):
     rows) fused into the step kernel (q4_hip_qsa_step_prep_batch), against
     the same step done as q_prep + k_prep per layer then the batched step."""
     rt, lib = b.rt, b.lib
+    assert b.R >= sets, "config_prep needs a Bench of >= 4 sets"
     L = b.L
     qg = rt.alloc(sets * L * N_HEAD * 2 * HD * 4)
     b.gen(qg, sets * L * N_HEAD * 2 * HD, 91)

@@ -14,6 +14,8 @@
 #include <stdlib.h>
 #include <unistd.h>
 
+#include <thread>
+
 #include "q4kv_internal.h"
 
 extern "C" {
@@ -21,6 +23,10 @@ extern "C" {
 }
 
 #define Q4KV_PIPE_NBUF 3
+/* threads per chunk of file I/O: one thread's pread/pwrite through the page
+ * cache is memcpy-bound well below the host link */
+#define Q4KV_PIPE_IO_THREADS 4
+#define Q4KV_PIPE_IO_MIN (4u << 20) /* smaller chunks stay on one thread */
 
 struct q4kv_pipe {
     uint8_t *buf[Q4KV_PIPE_NBUF];
@@ -58,6 +64,39 @@ static bool write_full(int fd, const uint8_t *p, uint64_t n, uint64_t off) {
     return true;
 }
 
+/* n bytes at file offset off, split into Q4KV_PIPE_IO_THREADS contiguous
+ * parts moved concurrently (the calling thread takes the first part). */
+template <bool READ>
+static bool io_par(int fd, uint8_t *p, uint64_t n, uint64_t off) {
+    if (n < Q4KV_PIPE_IO_MIN)
+        return READ ? read_full(fd, p, n, off) : write_full(fd, p, n, off);
+    const uint64_t part = (n / Q4KV_PIPE_IO_THREADS + 4095u) & ~(uint64_t)4095u;
+    bool ok[Q4KV_PIPE_IO_THREADS];
+    std::thread th[Q4KV_PIPE_IO_THREADS];
+    for (int t = 1; t < Q4KV_PIPE_IO_THREADS; t++) {
+        const uint64_t b = part * t, e = b + part < n ? b + part : n;
+        ok[t] = true;
+        if (b >= n) continue;
+        try {
+            th[t] = std::thread([=, &ok] {
+                ok[t] = READ ? read_full(fd, p + b, e - b, off + b)
+                             : write_full(fd, p + b, e - b, off + b);
+            });
+        } catch (...) { /* no thread: this part runs here */
+            ok[t] = READ ? read_full(fd, p + b, e - b, off + b)
+                         : write_full(fd, p + b, e - b, off + b);
+        }
+    }
+    ok[0] = READ ? read_full(fd, p, part < n ? part : n, off)
+                 : write_full(fd, p, part < n ? part : n, off);
+    bool all = ok[0];
+    for (int t = 1; t < Q4KV_PIPE_IO_THREADS; t++) {
+        if (th[t].joinable()) th[t].join();
+        all = all && ok[t];
+    }
+    return all;
+}
+
 /* Wait for buffer i's copy; for a pending save, write its bytes out. */
 static bool retire(q4kv_pipe *p, unsigned i) {
     if (!p->busy[i]) return true;
@@ -66,7 +105,7 @@ static bool retire(q4kv_pipe *p, unsigned i) {
         (void)hipGetLastError();
         return false;
     }
-    if (p->fd[i] >= 0 && !write_full(p->fd[i], p->buf[i], p->len[i], p->off[i])) return false;
+    if (p->fd[i] >= 0 && !io_par<false>(p->fd[i], p->buf[i], p->len[i], p->off[i])) return false;
     return true;
 }
 
@@ -113,7 +152,7 @@ extern "C" bool q4kv_pipe_file_to_dev(q4kv_pipe *p, int fd, uint64_t off, void *
     for (uint64_t o = 0; o < n; o += p->chunk) {
         const uint64_t len = n - o < p->chunk ? n - o : p->chunk;
         const unsigned i = p->next++ % Q4KV_PIPE_NBUF;
-        if (!retire(p, i) || !read_full(fd, p->buf[i], len, off + o) ||
+        if (!retire(p, i) || !io_par<true>(fd, p->buf[i], len, off + o) ||
             hipMemcpyAsync(d + o, p->buf[i], len, hipMemcpyHostToDevice, q4kv_stream) !=
                 hipSuccess ||
             hipEventRecord(p->ev[i], q4kv_stream) != hipSuccess) {
