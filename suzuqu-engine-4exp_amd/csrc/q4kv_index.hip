@@ -480,17 +480,19 @@ __device__ inline uint32_t xkey(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-union TopkHist {
-    uint32_t rep[256 * 32];          /* full path: 256 bins x 32 copies */
-    uint32_t dist[TK_DBINS * 32];    /* distance bins x 32 copies */
+/* HC histogram copies per bin (lane & (HC - 1) picks one: with 32, a
+ * half-wave's atomics land on distinct banks); CAP candidate capacity. */
+template <uint32_t HC, uint32_t CAP> union TopkHist {
+    uint32_t rep[256 * HC];          /* full path: 256 bins x HC copies */
+    uint32_t dist[TK_DBINS * HC];    /* distance bins x HC copies */
     uint32_t cand[1u << TK_CBITS];   /* candidate passes */
 };
-struct TopkSmem {
-    TopkHist h;
+template <uint32_t HC, uint32_t CAP> struct TopkSmem {
+    TopkHist<HC, CAP> h;
     uint32_t cg[TK_T], ce[TK_T];     /* per (key row, wave) counts -> offsets */
     uint64_t wm[TK_T];               /* per (key row, wave) candidate lane masks */
-    uint32_t ckey[TK_CAP];           /* candidates in index order */
-    int32_t cidx[TK_CAP];
+    uint32_t ckey[CAP];              /* candidates in index order */
+    int32_t cidx[CAP];
     uint32_t bins[TK_DBINS];
     uint32_t wtot[3][16];
     int32_t chosen[TK_MAXK];
@@ -585,13 +587,22 @@ __device__ inline uint32_t lanes_below(uint64_t m) {
  * device position's single row, or item t of a batch of descriptors. */
 enum { TK_ROWS = 0, TK_DEV = 1, TK_BATCH = 2 };
 
+/* Rows of up to 8 keys per thread (8192 blocks) take a smaller instance: 8
+ * histogram copies and 2048 candidates, so that two workgroups share a CU. */
+template <uint32_t KPT> struct TopkShape {
+    static constexpr uint32_t HC = KPT <= 8u ? 8u : 32u;
+    static constexpr uint32_t CAP = KPT <= 8u ? 2048u : TK_CAP;
+    static constexpr int WG_PER_CU = KPT <= 8u ? 2 : 1;
+};
+
 template <int SRC, uint32_t KPT>
-__global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *sel,
+__global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(const float *score, int32_t *sel,
                                                    uint32_t stride, uint32_t k_blk,
                                                    uint32_t ratio, uint32_t pos0,
                                                    uint32_t width, const int32_t *pp,
                                                    const q4kv_index_desc *descs) {
-    __shared__ TopkSmem sm;
+    constexpr uint32_t HC = TopkShape<KPT>::HC, CAP = TopkShape<KPT>::CAP;
+    __shared__ TopkSmem<HC, CAP> sm;
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
     uint32_t pos;
@@ -636,7 +647,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
 
     bool fast = nchunk == 1;
     if (fast) {
-        for (uint32_t i = tid; i < TK_DBINS * 32; i += TK_T) sm.h.dist[i] = 0;
+        for (uint32_t i = tid; i < TK_DBINS * HC; i += TK_T) sm.h.dist[i] = 0;
         sm.wm[tid] = 0;
         load_chunk(0);
         /* ---- row maximum (as the loads land) ---- */
@@ -653,16 +664,16 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
          * steps of |score| (the keys' bits above bit 19), clamped at 511;
          * 32 copies keep a half-wave's atomics on distinct banks ---- */
         const uint32_t Mb = M >> TK_DSHIFT;
-        uint32_t *hc = sm.h.dist + (lane & 31u);
+        uint32_t *hc = sm.h.dist + (lane & (HC - 1u));
 #pragma unroll
         for (uint32_t r = 0; r < KPT; r++)
-            atomicAdd(hc + min(Mb - (key[r] >> TK_DSHIFT), TK_DBINS - 1u) * 32u, 1u);
+            atomicAdd(hc + min(Mb - (key[r] >> TK_DSHIFT), TK_DBINS - 1u) * HC, 1u);
         __syncthreads();
         { /* fold the copies: two threads per bin */
-            const uint32_t *hp = sm.h.dist + (tid >> 1) * 32u + (tid & 1u) * 16u;
+            const uint32_t *hp = sm.h.dist + (tid >> 1) * HC + (tid & 1u) * (HC / 2u);
             uint32_t v = 0;
 #pragma unroll
-            for (int i = 0; i < 16; i++) v += hp[i];
+            for (uint32_t i = 0; i < HC / 2u; i++) v += hp[i];
             v += __shfl_xor(v, 1);
             if ((tid & 1u) == 0) sm.bins[tid >> 1] = v;
         }
@@ -685,7 +696,7 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         __syncthreads();
         const uint32_t B = sm.st[0], above = sm.st[1], ncand = sm.st[2];
         /* the clamped last bin and the padding keys' bin take the full path */
-        fast = B < min(Mb, TK_DBINS - 1u) && ncand <= TK_CAP;
+        fast = B < min(Mb, TK_DBINS - 1u) && ncand <= CAP;
         const uint32_t Kc = (Mb - B) << TK_DSHIFT; /* candidates: key >= Kc */
         if (fast) {
             /* ---- ordered compaction of the candidates: each lane's 64-bit
@@ -781,11 +792,11 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
         /* ---- full path: four 8-bit radix passes over every key ---- */
         if (tid == 0) { sm.st[4] = 0; sm.st[5] = 0; }
         for (uint32_t pass = 0; pass < 4; pass++) {
-            for (uint32_t i = tid; i < 256 * 32; i += TK_T) sm.h.rep[i] = 0;
+            for (uint32_t i = tid; i < 256 * HC; i += TK_T) sm.h.rep[i] = 0;
             __syncthreads();
             const uint32_t sh = 24u - 8u * pass;
             const uint32_t pre = sm.st[4];
-            uint32_t *hcopy = sm.h.rep + (lane & 31u);
+            uint32_t *hcopy = sm.h.rep + (lane & (HC - 1u));
             for (uint32_t c = 0; c < nchunk; c++) {
                 if (nchunk > 1) load_chunk(c);
 #pragma unroll
@@ -793,16 +804,16 @@ __global__ __launch_bounds__(1024) void qsa_topk_k(const float *score, int32_t *
                     const uint32_t u = key[r];
                     /* digits above this pass must equal the prefix found so
                      * far (pass 0: the empty prefix, (u >> 8) >> 24 == 0) */
-                    if (((u >> 8) >> sh) == pre) atomicAdd(hcopy + ((u >> sh) & 255u) * 32u, 1u);
+                    if (((u >> 8) >> sh) == pre) atomicAdd(hcopy + ((u >> sh) & 255u) * HC, 1u);
                 }
             }
             __syncthreads();
-            { /* fold the 32 copies: four lanes per bin, eight copies each */
+            { /* fold the copies: four lanes per bin, HC / 4 copies each */
                 const uint32_t bin = tid >> 2, part = tid & 3u;
-                const uint32_t *hp = sm.h.rep + bin * 32u + part * 8u;
+                const uint32_t *hp = sm.h.rep + bin * HC + part * (HC / 4u);
                 uint32_t v = 0;
 #pragma unroll
-                for (int i = 0; i < 8; i++) v += hp[i];
+                for (uint32_t i = 0; i < HC / 4u; i++) v += hp[i];
                 v += __shfl_xor(v, 1);
                 v += __shfl_xor(v, 2);
                 if (part == 0) sm.bins[bin] = v;
@@ -1085,7 +1096,11 @@ extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok
     (void)hipGetLastError();
     /* the longest row decides the register layout */
     const uint64_t vis_max = ((uint64_t)pos0 + n_tok) / ratio;
-    if (vis_max <= 16u * TK_T)
+    if (vis_max <= 8u * TK_T)
+        qsa_topk_k<TK_ROWS, 8><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk,
+                                                                 ratio, pos0, width, nullptr,
+                                                                 nullptr);
+    else if (vis_max <= 16u * TK_T)
         qsa_topk_k<TK_ROWS, 16><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk,
                                                                   ratio, pos0, width, nullptr,
                                                                   nullptr);
