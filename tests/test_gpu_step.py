@@ -111,12 +111,16 @@ def _sel_kv(rng, s, pos):
     return np.stack([selection(rng, pos) for _ in range(N_KVH)])
 
 
-def test_step_batch_q8_matches_append_then_decode(rt, oracle):
-    """12 layers, new position inside each list (the list's last entry)."""
-    rng = np.random.default_rng(900)
+# 12 sequences (24 items): two 64-position chunks per workgroup, the
+# single-buffer kernel; 32 sequences (64 items): five chunks per workgroup,
+# the double-buffered instance (fused step and batched decode alike)
+@pytest.mark.parametrize("n_seq", [12, 32])
+def test_step_batch_q8_matches_append_then_decode(rt, oracle, n_seq):
+    """n_seq layers, new position inside each list (the list's last entry)."""
+    rng = np.random.default_rng(900 + n_seq)
     ctx = 16384
-    items, _ = _case(rng, oracle, 12, ctx, q4kv.KV_Q8, lambda s: ctx - 1 - 600 * s, _sel_kv)
-    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what="q8 12 layers")
+    items, _ = _case(rng, oracle, n_seq, ctx, q4kv.KV_Q8, lambda s: ctx - 1 - 300 * s, _sel_kv)
+    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what=f"q8 {n_seq} layers")
 
 
 def test_step_batch_position_anywhere_in_list(rt, oracle):

@@ -90,7 +90,8 @@ def _run(rt, items, ctx, fused):
     return res
 
 
-@pytest.mark.parametrize("n_seq,ctx,width", [(12, 16384, 0), (3, 4096, 40)])
+# 32 sequences: five chunks per workgroup, the double-buffered instance
+@pytest.mark.parametrize("n_seq,ctx,width", [(12, 16384, 0), (3, 4096, 40), (32, 16384, 0)])
 def test_step_prep_matches_prep_then_step(rt, oracle, n_seq, ctx, width):
     """12 layers of 2051-entry lists (split-KV with a merge), and 40-entry
     lists (one split: the kernel's own epilogue applies the gate)."""
