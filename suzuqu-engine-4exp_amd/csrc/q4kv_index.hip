@@ -669,11 +669,13 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         for (uint32_t r = 0; r < KPT; r++)
             atomicAdd(hc + min(Mb - (key[r] >> TK_DSHIFT), TK_DBINS - 1u) * HC, 1u);
         __syncthreads();
-        { /* fold the copies: two threads per bin */
+        { /* fold the copies: two threads per bin, each reading its half in an
+           * order rotated by the bin, so a wave's reads spread over the banks
+           * (in order, lanes 16 dwords apart would meet 16 to a bank) */
             const uint32_t *hp = sm.h.dist + (tid >> 1) * HC + (tid & 1u) * (HC / 2u);
             uint32_t v = 0;
 #pragma unroll
-            for (uint32_t i = 0; i < HC / 2u; i++) v += hp[i];
+            for (uint32_t i = 0; i < HC / 2u; i++) v += hp[(i + (tid >> 1)) & (HC / 2u - 1u)];
             v += __shfl_xor(v, 1);
             if ((tid & 1u) == 0) sm.bins[tid >> 1] = v;
         }
@@ -808,12 +810,13 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                 }
             }
             __syncthreads();
-            { /* fold the copies: four lanes per bin, HC / 4 copies each */
+            { /* fold the copies: four lanes per bin, HC / 4 copies each, read
+               * in an order rotated by the bin (bank spread, as above) */
                 const uint32_t bin = tid >> 2, part = tid & 3u;
                 const uint32_t *hp = sm.h.rep + bin * HC + part * (HC / 4u);
                 uint32_t v = 0;
 #pragma unroll
-                for (uint32_t i = 0; i < HC / 4u; i++) v += hp[i];
+                for (uint32_t i = 0; i < HC / 4u; i++) v += hp[(i + bin) & (HC / 4u - 1u)];
                 v += __shfl_xor(v, 1);
                 v += __shfl_xor(v, 2);
                 if (part == 0) sm.bins[bin] = v;
