@@ -1241,8 +1241,10 @@ __global__ __launch_bounds__(256) void qsa_comb_k(AttnArgs a) {
     float L = 0.f, acc = 0.f;
     if (S <= 8u) acc = comb_reg<8>(pb, sst, S, col, L);
     else if (S <= 16u) acc = comb_reg<16>(pb, sst, S, col, L);
+    else if (S <= 20u) acc = comb_reg<20>(pb, sst, S, col, L);
     else if (S <= 24u) acc = comb_reg<24>(pb, sst, S, col, L);
     else if (S <= 32u) acc = comb_reg<32>(pb, sst, S, col, L);
+    else if (S <= 36u) acc = comb_reg<36>(pb, sst, S, col, L);
     else if (S <= 48u) acc = comb_reg<48>(pb, sst, S, col, L);
     else if (S <= COMB_REG) acc = comb_reg<COMB_REG>(pb, sst, S, col, L);
     else {
@@ -1295,8 +1297,10 @@ __global__ __launch_bounds__(256) void qsa_comb_gemv_k(AttnArgs a, const q4kv_ou
         float L = 0.f, acc;
         if (S <= 8u) acc = comb_reg<8>(pb, sst, S, tid, L);
         else if (S <= 16u) acc = comb_reg<16>(pb, sst, S, tid, L);
+        else if (S <= 20u) acc = comb_reg<20>(pb, sst, S, tid, L);
         else if (S <= 24u) acc = comb_reg<24>(pb, sst, S, tid, L);
         else if (S <= 32u) acc = comb_reg<32>(pb, sst, S, tid, L);
+        else if (S <= 36u) acc = comb_reg<36>(pb, sst, S, tid, L);
         else if (S <= 48u) acc = comb_reg<48>(pb, sst, S, tid, L);
         else if (S <= COMB_REG) acc = comb_reg<COMB_REG>(pb, sst, S, tid, L);
         else {
