@@ -4,6 +4,8 @@
   position's dequantised V row (times sigmoid(gate) when a gate is given);
 - identical keys: all scores equal, so the output is the mean of the listed
   V rows;
+- a list with no valid entry (all padding or out of range): every split
+  holds l = 0, and the merged output is 0, gated or not;
 - the split-KV division does not change the result: one item alone (many
   splits) and the same item inside a 24-item batch (fewer splits each) agree.
 
@@ -72,6 +74,44 @@ def test_single_valid_position_returns_its_v_row(rt, oracle):
             want = vd[pos[h // GQA], h // GQA] * sig
             np.testing.assert_allclose(got[0, h], want, rtol=1e-5, atol=1e-6,
                                        err_msg=f"gated, slot {slot} head {h}")
+
+
+def test_list_without_valid_entries_gives_zero(rt, oracle):
+    rng = np.random.default_rng(903)
+    ctx = 262144
+    k, v = heads(rng, (4096, N_KVH)), heads(rng, (4096, N_KVH))
+    kc = rt.alloc(ctx * N_KVH * 272)
+    vc = rt.alloc(ctx * N_KVH * 272)
+    for dst, x in ((kc, k), (vc, v)):
+        rt.h2d(dst, oracle.quant_q8(x))
+    idx = np.full((N_KVH, WIDTH), -1, np.int32)
+    idx[:, ::3] = ctx + 7  # out of range: skipped like padding
+    q = heads(rng, (1, N_HEAD))
+    gate = rng.standard_normal((1, N_HEAD, HD)).astype(np.float32)
+    for g in (None, gate):
+        note(f"no valid entry, gate={'yes' if g is not None else 'no'}")
+        got = _decode_idx_kv(rt, q, kc, vc, idx.ravel(), WIDTH, ctx, gate=g)
+        assert np.isfinite(got).all() and not got.any()
+    # the same through the batched entry point, 12 items
+    items = 12
+    qs = heads(rng, (items, N_HEAD))
+    dq, di = rt.upload(qs), rt.upload(idx)
+    dout = rt.alloc(qs.nbytes)
+    rt.h2d(dout, np.full(qs.size, np.nan, np.float32))
+    descs = (q4kv.SeqDesc * items)()
+    qb = N_HEAD * HD * 4
+    for i in range(items):
+        descs[i] = q4kv.SeqDesc(kc, vc, dq + i * qb, None, dout + i * qb, di, WIDTH, WIDTH,
+                                ctx, 0)
+    dd = rt.alloc(ctypes.sizeof(descs))
+    assert rt.lib.q4_hip_h2d(dd, ctypes.addressof(descs), ctypes.sizeof(descs))
+    assert rt.lib.q4_hip_qsa_decode_batch(dd, items, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8,
+                                          WIDTH)
+    rt.sync()
+    got = rt.download(dout, qs.nbytes, np.float32)
+    assert np.isfinite(got).all() and not got.any()
+    for p in (kc, vc, dq, di, dout, dd):
+        rt.free(p)
 
 
 def test_identical_keys_give_the_mean_of_v(rt, oracle):
