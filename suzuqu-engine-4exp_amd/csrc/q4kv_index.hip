@@ -477,7 +477,8 @@ constexpr uint32_t TK_CBITS = 10;      /* widest digit of the candidate passes *
 /* Order-preserving uint32 key (src/q4_rocm.cu:7471-7474). */
 __device__ inline uint32_t xkey(float f) {
     const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    /* negative: all bits flipped; otherwise the sign bit set */
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
 
 /* HC histogram copies per bin (lane & (HC - 1) picks one: with 32, a
