@@ -332,6 +332,30 @@ __device__ static inline float row16_max(float v) {
     v = fmax2(v, dppf<0x141>(v)); /* row_half_mirror */
     return fmax2(v, dppf<0x140>(v)); /* row_mirror */
 }
+/* Maxima of four values over their DPP rows, one v_max_f32_dpp per step. The
+ * compiler folds fmed3(a, b, +inf) back into maxnum and then canonicalises
+ * both operands of every max (three instructions a step), so the steps are
+ * written out: the four chains interleave, which gives each DPP read the two
+ * wait states it needs after the previous write of its source; the s_nop
+ * covers the first step. Operands are scores or -inf, never NaN. */
+__device__ static inline void row16_max4(float (&v)[4]) {
+#define Q4KV_DPPMAX4(CTL)                                                                      \
+    "v_max_f32_dpp %0, %0, %0 " CTL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"            \
+    "v_max_f32_dpp %1, %1, %1 " CTL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"            \
+    "v_max_f32_dpp %2, %2, %2 " CTL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"            \
+    "v_max_f32_dpp %3, %3, %3 " CTL " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+    asm("s_nop 1\n\t" Q4KV_DPPMAX4("quad_perm:[1,0,3,2]") Q4KV_DPPMAX4("quad_perm:[2,3,0,1]")
+            Q4KV_DPPMAX4("row_half_mirror") Q4KV_DPPMAX4("row_mirror")
+        : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+#undef Q4KV_DPPMAX4
+}
+/* max(a, b, c) in one v_max3_f32, without the canonicalisations (non-NaN
+ * operands). */
+__device__ static inline float fmax3v(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 __device__ static inline float row16_sum(float v) {
     v += dppf<0xB1>(v);
     v += dppf<0x4E>(v);
@@ -1045,14 +1069,17 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         }
         TRACE(4);
         const bool valid = spos[r] >= 0;
-        float T[4];
+        float T[4], cm[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
             const float t = pair32_sum(S[i]) * a.scale_log2;
             T[i] = valid ? t : -INFINITY;
-            const float cm = row16_max(T[i]);
-            if (mrow == 0 && jg < 2u) s_cmax[wave][4u * jg + i] = cm;
+            cm[i] = T[i];
         }
+        row16_max4(cm);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++)
+            if (mrow == 0 && jg < 2u) s_cmax[wave][4u * jg + i] = cm[i];
         TRACE(5);
         __syncthreads();
         TRACE(6);
@@ -1060,9 +1087,8 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
             const uint32_t h = (4u * jg + i) & 7u;
-            const float cm = fmax2(fmax2(s_cmax[0][h], s_cmax[1][h]),
-                                   fmax2(s_cmax[2][h], s_cmax[3][h]));
-            const float mn = fmax2(m_run[i], cm);
+            const float mn = fmax3v(fmax3v(s_cmax[0][h], s_cmax[1][h], s_cmax[2][h]),
+                                    s_cmax[3][h], m_run[i]);
             /* exp2(-inf) = 0 handles masked scores and the first chunk; a
              * still-empty max is shifted to 0 so that -inf - -inf is avoided */
             const float ms = mn == -INFINITY ? 0.f : mn;
