@@ -58,6 +58,32 @@ LAYER_B = GATHER_B + IDX_B + 2 * QO_B + APPEND_B  # 2 285 848 B
 SPLIT_KERNEL_B = GATHER_B + IDX_B + QO_B + APPEND_B
 
 
+def uniform_rows(rng, lo, hi, k):
+    """Per row r, k distinct positions drawn uniformly from [lo, hi[r]),
+    sorted. Vectorised: oversample with replacement, keep the distinct
+    values (a uniform random subset given its size), then a uniform random
+    k of them; rows with too few distinct draws are drawn again."""
+    hi = np.asarray(hi, np.int64)
+    out = np.empty((hi.size, k), np.int64)
+    todo = np.arange(hi.size)
+    while todo.size:
+        span = hi[todo] - lo
+        assert (span >= k).all()
+        m = k + k // 4 + 64
+        x = rng.integers(0, span[:, None], size=(todo.size, m), dtype=np.int64)
+        x.sort(axis=1)
+        dup = x[:, 1:] == x[:, :-1]
+        keys = rng.random(x.shape, dtype=np.float32)
+        keys[:, 1:][dup] = 2.0  # repeated values are never picked
+        ok = (~dup).sum(axis=1) + 1 >= k
+        pick = np.argpartition(keys, k - 1, axis=1)[:, :k]
+        pick.sort(axis=1)
+        rows = np.take_along_axis(x, pick, axis=1) + lo
+        out[todo[ok]] = rows[ok]
+        todo = todo[~ok]
+    return out
+
+
 def selection(rng, pos):
     n_uni = WIDTH - 3 - 512
     uni = rng.choice(pos - 512 - 2, size=n_uni, replace=False).astype(np.int64) + 3
@@ -79,6 +105,10 @@ class Bench:
                                                C.c_uint32, C.c_uint32, C.c_uint32, C.c_int]
 
         def gen(ptr, n, seed):
+            # the generator launches on the null stream, which does not order
+            # against the library's non-blocking stream: drain that first so
+            # no queued kernel still reads the buffer being rewritten
+            rt.sync()
             assert synth.q4kv_synth_heads(ptr, n, HD, seed, *OUTLIERS) == 0
 
         self.gen = gen
@@ -144,16 +174,16 @@ class Bench:
             1.0 / 16, q4kv.KV_Q8, WIDTH)
 
     def step_batched(self, s):
-        """One decode step of all layers: a captured graph (the fused append +
-        split-KV kernel and the merge), one graph launch per step."""
+        """One decode step of all layers: one q4_hip_qsa_step_batch call (the
+        fused append + split-KV kernel, then the merge) enqueued directly on
+        the library stream."""
+        assert self._enqueue_batched(s)
+
+    def step_batched_graph(self, s):
+        """The same step replayed from a captured graph (one per selection
+        set)."""
         if self.bgraphs is None:
-            self.bgraphs = []
-            for r in range(self.R):
-                assert self.lib.q4_hip_graph_begin() == 1
-                ok = self._enqueue_batched(r)
-                g = self.lib.q4_hip_graph_end()
-                assert ok and g, "graph capture failed"
-                self.bgraphs.append(g)
+            self.bgraphs = _graphs(self.lib, self._enqueue_batched, self.R)
         assert self.lib.q4_hip_graph_launch(self.bgraphs[s])
 
     def kernel_time(self, rounds=8):
@@ -195,19 +225,22 @@ class Bench:
         return ok
 
     def step_sequential(self, s):
+        """Per layer: q4_hip_kv_append_d then q4_hip_qsa_decode_idx_kv (the
+        reference's call sequence, src/q4_fwd.c:891,922), enqueued directly."""
+        self.lib.q4_hip_pos_push(self.pos[s])
+        assert self._enqueue_sequential(s)
+
+    def step_sequential_graph(self, s):
+        """The same per-layer calls replayed from a captured graph."""
         if self.graphs is None:
-            self.graphs = []
-            for r in range(self.R):
-                assert self.lib.q4_hip_graph_begin() == 1
-                ok = self._enqueue_sequential(r)
-                g = self.lib.q4_hip_graph_end()
-                assert ok and g, "graph capture failed"
-                self.graphs.append(g)
+            self.graphs = _graphs(self.lib, self._enqueue_sequential, self.R)
         self.lib.q4_hip_pos_push(self.pos[s])
         assert self.lib.q4_hip_graph_launch(self.graphs[s])
 
     def timed(self, step, steps, warmup, prof=False):
-        for i in range(warmup):
+        # every selection set (and its graph, where one is used) runs at least
+        # once before the timed region, whatever the warmup count
+        for i in range(max(warmup, self.R)):
             step(i % self.R)
         self.rt.sync()
         if prof:
@@ -297,6 +330,8 @@ class Bench:
             "openmp": {"threads": threads, "value": round(nt * LAYER_B / elt / 1e9, 4),
                        "us_per_layer": round(elt / nt * 1e6, 1)},
             "host_cpu": _cpu_model(),
+            "host_nproc": len(os.sched_getaffinity(0)),
+            "host_logical_cpus": os.cpu_count(),
         }
         return res, cpu
 
@@ -320,7 +355,7 @@ def _graphs(lib, enqueue, n):
 
 def _time_graphs(b, graphs, steps):
     lib = b.lib
-    for i in range(8):
+    for i in range(max(8, len(graphs))):
         assert lib.q4_hip_graph_launch(graphs[i % len(graphs)])
     b.rt.sync()
     t0 = time.perf_counter()
@@ -331,6 +366,25 @@ def _time_graphs(b, graphs, steps):
     for g in graphs:
         lib.q4_hip_graph_free(g)
     return wall / steps
+
+
+def _time_direct(b, enqueue, n_sets, steps):
+    """Seconds per step with each step's calls enqueued directly (no graph)."""
+    for i in range(max(8, n_sets)):
+        assert enqueue(i % n_sets)
+    b.rt.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        assert enqueue(i % n_sets)
+    b.rt.sync()
+    return (time.perf_counter() - t0) / steps
+
+
+def _time_both(b, enqueue, n_sets, steps):
+    """(direct, graph) seconds per step."""
+    t_d = _time_direct(b, enqueue, n_sets, steps)
+    t_g = _time_graphs(b, _graphs(b.lib, enqueue, n_sets), steps)
+    return t_d, t_g
 
 
 def _fill(b, ptr, n_tok, kind, seed):
@@ -349,7 +403,7 @@ def _fill(b, ptr, n_tok, kind, seed):
     rt.free(tmp)
 
 
-def config2(b, steps=200, sets=4):
+def config2(b, steps=200, sets=10):
     """Config 2: 32 sequences, contexts log-uniform in [8192, 131072], own
     q8_0 caches; one step = every sequence's append + sparse attention
     (q4_hip_qsa_step_batch)."""
@@ -389,9 +443,8 @@ def config2(b, steps=200, sets=4):
     dd = rt.alloc(C.sizeof(steps_d))
     assert lib.q4_hip_h2d(dd, C.addressof(steps_d), C.sizeof(steps_d))
     sz = C.sizeof(q4kv.StepDesc)
-    graphs = _graphs(lib, lambda r: lib.q4_hip_qsa_step_batch(
-        dd + r * n_seq * sz, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH), sets)
-    t = _time_graphs(b, graphs, steps)
+    t, t_graph = _time_both(b, lambda r: lib.q4_hip_qsa_step_batch(
+        dd + r * n_seq * sz, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH), sets, steps)
     byts = n_seq * LAYER_B
     for kc, vc, _ in caches:
         rt.free(kc)
@@ -400,9 +453,12 @@ def config2(b, steps=200, sets=4):
         rt.free(p_)
     return {"what": "32 sequences (ctx log-uniform 8192-131072, seed 1236), one batched decode "
                     "step each: q8_0 append + sparse attention over 2x2051 positions",
-            "us_per_step": round(t * 1e6, 2), "bytes_per_step": byts,
+            "us_per_step": round(t * 1e6, 2), "graph_us_per_step": round(t_graph * 1e6, 2),
+            "bytes_per_step": byts,
             "gbs": round(byts / t / 1e9, 1), "pct_of_peak": round(100 * byts / t / 1e9 / PEAK_GBS, 2),
-            "steps": steps, "selection_sets": sets}
+            "steps": steps, "selection_sets": sets,
+            "gathered_bytes_rotated": sets * byts,
+            "note": "sets rotate so the rows gathered across sets exceed the 256 MB Infinity Cache"}
 
 
 def config3(b, reps=4):
@@ -420,21 +476,15 @@ def config3(b, reps=4):
     b.gen(nv, chunk * N_KVH * HD, 4003)
     dq, dout = rt.alloc(chunk * QO_B), rt.alloc(chunk * QO_B)
     b.gen(dq, chunk * N_HEAD * HD, 4004)
-    # lists: the 1536 earlier positions of query t per KV head are a strided
-    # pseudo-random permutation of [3, pos-511) (distinct, then sorted)
+    # lists: 3 sinks + 1536 distinct positions drawn uniformly from
+    # [3, pos - 511) + the 512 most recent, per query and KV head (the rule
+    # tests/synth.py:selection applies)
     rng = np.random.default_rng(1237)
     pos = ctx0 + np.arange(chunk, dtype=np.int64)
-    span = pos - 511 - 3
     sel = np.empty((chunk, N_KVH, WIDTH), np.int32)
-    i = np.arange(1536, dtype=np.int64)
     for h in range(N_KVH):
-        start = rng.integers(0, span)
-        step = rng.integers(1, span)
-        step = np.where(np.gcd(step, span) == 1, step, 1)
-        uni = 3 + (start[:, None] + step[:, None] * i[None, :]) % span[:, None]
-        uni.sort(axis=1)
         sel[:, h, :3] = np.arange(3)
-        sel[:, h, 3:1539] = uni
+        sel[:, h, 3:1539] = uniform_rows(rng, 3, pos - 511, 1536)
         sel[:, h, 1539:] = pos[:, None] - 511 + np.arange(512)[None, :]
     dsel = rt.upload(sel)
     off = ctx0 * BPT
@@ -458,19 +508,19 @@ def config3(b, reps=4):
         rt.free(p_)
     return {"what": "8192-token q8_0 chunk appended to a 16384-token cache, then 8192 "
                     "queries x 16 heads over per-KV-head lists of 2051 (3 sinks + 512 recent "
-                    "+ 1536 earlier, strided pseudo-random)",
+                    "+ 1536 distinct uniform earlier positions)",
             "us_per_layer": round(wall * 1e6, 1), "gflop": round(flop / 1e9, 1),
             "tflops": round(flop / wall / 1e12, 2),
             "pct_of_fp16_mfma_peak": round(100 * flop / wall / 2.5e15, 2), "reps": reps}
 
 
-def config4(b, steps=100, sets=4, layers=4):
+def config4(b, steps=100, sets=16, layers=12):
     """Config 4: config 1's decode step on f16 and f32 caches, and the
     restore of a 100000-token x 12-layer q8_0 session image from pinned host
     memory."""
     rt, lib = b.rt, b.lib
     # the descriptors address the Bench's per-(set, layer) rows and outputs
-    assert b.L >= layers and b.R >= sets, "config4 needs a Bench of >= 4 layers and sets"
+    layers, sets = min(layers, b.L), min(sets, b.R)
     out = {}
     for kind, name in ((q4kv.KV_F16, "f16"), (q4kv.KV_F32, "f32")):
         bpt = q4kv.token_bytes(kind, N_KVH, HD)
@@ -490,12 +540,14 @@ def config4(b, steps=100, sets=4, layers=4):
         dd = rt.alloc(C.sizeof(steps_d))
         assert lib.q4_hip_h2d(dd, C.addressof(steps_d), C.sizeof(steps_d))
         sz = C.sizeof(q4kv.StepDesc)
-        graphs = _graphs(lib, lambda r: lib.q4_hip_qsa_step_batch(
-            dd + r * layers * sz, layers, N_HEAD, N_KVH, HD, 1.0 / 16, kind, WIDTH), sets)
-        t = _time_graphs(b, graphs, steps) / layers
+        t, t_graph = _time_both(b, lambda r: lib.q4_hip_qsa_step_batch(
+            dd + r * layers * sz, layers, N_HEAD, N_KVH, HD, 1.0 / 16, kind, WIDTH), sets, steps)
+        t, t_graph = t / layers, t_graph / layers
         byts = 2 * N_KVH * WIDTH * (bpt // N_KVH) + IDX_B + 2 * QO_B + 2 * N_KVH * HD * 4 + 2 * bpt
-        out[name] = {"us_per_layer": round(t * 1e6, 3), "bytes_per_layer": byts,
-                     "gbs": round(byts / t / 1e9, 1), "layers_per_step": layers}
+        out[name] = {"us_per_layer": round(t * 1e6, 3),
+                     "graph_us_per_layer": round(t_graph * 1e6, 3), "bytes_per_layer": byts,
+                     "gbs": round(byts / t / 1e9, 1), "layers_per_step": layers,
+                     "selection_sets": sets, "gathered_bytes_rotated": sets * layers * byts}
         for p_ in kcs + vcs + [dd]:
             rt.free(p_)
     # session restore: 12 layers x 100000 tokens of q8_0 K and V from pinned memory
@@ -882,9 +934,11 @@ def main():
     kern_ms = None
     if args.mode in ("batched", "both"):
         res["batched"] = b.timed(b.step_batched, args.steps, args.warmup)
+        res["batched_graph"] = b.timed(b.step_batched_graph, args.steps, args.warmup)
         kern_ms = b.kernel_time()
     if args.mode in ("sequential", "both"):
         res["sequential"] = b.timed(b.step_sequential, args.steps, args.warmup)
+        res["sequential_graph"] = b.timed(b.step_sequential_graph, args.steps, args.warmup)
     g_us, g_gbs = b.gather_ceiling()
     configs = None
     if args.configs:
@@ -894,7 +948,7 @@ def main():
                    "out_projection_fused": config_out(b),
                    "indexer_decode": config_indexer(b),
                    "indexer_prefill": config_indexer_prefill(b)}
-    threads = min(16, os.cpu_count() or 1)
+    threads = min(16, len(os.sched_getaffinity(0)))
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
     head = "batched" if "batched" in res else "sequential"
     wall, gpu_s, _ = res[head]
@@ -909,7 +963,9 @@ def main():
         "config": {
             "workload": (f"config1 QSA sparse decode: {L} QSA layers x (q8_0 append + sparse "
                          f"attention), {CTX}-token q8_0 cache per layer, 16 Q / 2 KV heads, "
-                         f"hd 256, 2051 selected positions per KV head, {head} launch"),
+                         f"hd 256, 2051 selected positions per KV head, one "
+                         + ("q4_hip_qsa_step_batch call per step" if head == "batched" else
+                            "append + decode call pair per layer") + ", enqueued directly"),
             "kv": "q8_0", "ctx": CTX, "layers_per_step": L, "selection_sets": args.sets,
             "bytes_per_layer": LAYER_B, "parallelism": "single GPU",
         },
