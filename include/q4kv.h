@@ -186,6 +186,20 @@ bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32
                            uint32_t n_kvh, uint32_t hd, float scale, int kv_f16,
                            uint32_t max_n);
 
+/* q4_hip_qsa_step_batch without any allocation: no counterpart in the
+ * reference. For callers that cannot call hipMalloc (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid allocation). The split
+ * partials live in a static 16 MiB device array (one per GPU, held until
+ * the process ends; q4_hip_init resolves its address), so the call
+ * allocates nothing. Same arguments, same split division and results as
+ * q4_hip_qsa_step_batch, bit for bit. Returns false, with a message, when
+ * the call's partials would exceed 4M floats (n_seq * n_kvh items x splits x
+ * n_head/n_kvh x 258). Calls that overlap on one GPU share the array and
+ * race: order them on one stream. */
+bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uint32_t n_seq,
+                                   uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
+                                   int kv_f16, uint32_t max_n);
+
 /* A decode step with the query/key preparation fused in (src/q4_fwd.c:806-824:
  * q4_hip_qsa_q_prep + q4_hip_qsa_k_prep + the append + the attention, in
  * one launch plus the merge). step.seq.q points at the raw rows

@@ -1436,29 +1436,47 @@ struct OutProj {
     float y_scale;
 };
 
-template <int KIND, int MODE>
-static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa,
-                        const OutProj *op = nullptr) {
-    constexpr uint32_t CP = KCfg<KIND>::CP;
-    const uint32_t n_chunks = (max_n + CP - 1u) / CP;
+/* Where a launch's split partials go: the library's buffer (allocated by
+ * q4_hip_init), or the static scratch of the no-allocation entry point. */
+struct PartBuf {
+    float *ptr;
+    size_t cap; /* floats */
+};
+static PartBuf lib_part(void) { return PartBuf{q4kv_part, q4kv_part_cap}; }
+
+/* The split count S and chunks per split for n_items items of up to max_n
+ * list entries, bounded by a partial buffer of cap floats (0 or no buffer:
+ * one split, finalised in place). The same inputs always give the same
+ * division, so two entry points that share it give identical results. */
+static void choose_split(uint32_t n_items, uint32_t n_chunks, uint32_t gqa, bool have_part,
+                         size_t cap, uint32_t &S, uint32_t &cps) {
     /* Fill the chip once: the fast q8 kernel keeps 2 workgroups per CU
      * resident, the generic one about as many; more splits than that only
      * add a second round of workgroups and more partials to merge. */
-    const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
-    if (IS_STEP(MODE) && !fast) return false; /* the fused append needs the fast kernel */
-    uint32_t S = (split_target() + n_items - 1u) / n_items;
+    S = (split_target() + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
     if (S > COMB_MAXS) S = COMB_MAXS;
     const size_t per = (size_t)gqa * PSTRIDE;
-    while (S > 1u && (size_t)n_items * S * per > q4kv_part_cap) S--;
-    if (!q4kv_part) S = 1u;
-    const uint32_t cps = n_chunks ? (n_chunks + S - 1u) / S : 1u;
+    while (S > 1u && (size_t)n_items * S * per > cap) S--;
+    if (!have_part) S = 1u;
+    cps = n_chunks ? (n_chunks + S - 1u) / S : 1u;
     if (n_chunks) S = (n_chunks + cps - 1u) / cps;
     if (S < 1u) S = 1u;
+}
+
+template <int KIND, int MODE>
+static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa,
+                        const OutProj *op = nullptr, PartBuf pb = lib_part()) {
+    constexpr uint32_t CP = KCfg<KIND>::CP;
+    const uint32_t n_chunks = (max_n + CP - 1u) / CP;
+    const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
+    if (IS_STEP(MODE) && !fast) return false; /* the fused append needs the fast kernel */
+    uint32_t S, cps;
+    choose_split(n_items, n_chunks, gqa, pb.ptr != nullptr, pb.cap, S, cps);
     a.S = S;
     a.cps = cps;
-    a.part = q4kv_part;
+    a.part = pb.ptr;
     for (uint32_t i0 = 0; i0 < n_items; i0 += Q4KV_MAX_GRID_Y) {
         const uint32_t ni = n_items - i0 < Q4KV_MAX_GRID_Y ? n_items - i0 : Q4KV_MAX_GRID_Y;
         a.item0 = i0;
@@ -1492,12 +1510,13 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
 }
 
 template <int MODE>
-static bool launch_attn(int kind, const AttnArgs &a, uint32_t n_items, uint32_t max_n) {
+static bool launch_attn(int kind, const AttnArgs &a, uint32_t n_items, uint32_t max_n,
+                        PartBuf pb = lib_part()) {
     const uint32_t gqa = a.n_head / a.n_kvh;
     switch (kind) {
-    case Q4KV_Q8: return launch_kind<Q4KV_Q8, MODE>(a, n_items, max_n, gqa);
-    case Q4KV_F16: return launch_kind<Q4KV_F16, MODE>(a, n_items, max_n, gqa);
-    case Q4KV_F32: return launch_kind<Q4KV_F32, MODE>(a, n_items, max_n, gqa);
+    case Q4KV_Q8: return launch_kind<Q4KV_Q8, MODE>(a, n_items, max_n, gqa, nullptr, pb);
+    case Q4KV_F16: return launch_kind<Q4KV_F16, MODE>(a, n_items, max_n, gqa, nullptr, pb);
+    case Q4KV_F32: return launch_kind<Q4KV_F32, MODE>(a, n_items, max_n, gqa, nullptr, pb);
     default: return false;
     }
 }
@@ -1594,11 +1613,9 @@ extern "C" bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n
     return launch_attn<MODE_BATCH>(kv_f16, a, n_seq * n_kvh, max_n);
 }
 
-extern "C" bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq,
-                                      uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
-                                      int kv_f16, uint32_t max_n) {
-    if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
-        return false;
+static bool step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32_t n_head,
+                       uint32_t n_kvh, uint32_t hd, float scale, int kv_f16, uint32_t max_n,
+                       PartBuf pb) {
     (void)hipGetLastError();
     AttnArgs a = base_args(nullptr, nullptr, nullptr, nullptr, nullptr, n_head, n_kvh, hd, 0,
                            scale);
@@ -1606,11 +1623,83 @@ extern "C" bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_
     a.desc_stride = sizeof(q4kv_step_desc);
     const uint32_t gqa = n_head / n_kvh;
     if (kv_f16 == Q4KV_Q8 && hd == 256u && gqa <= 8u)
-        return launch_kind<Q4KV_Q8, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa);
+        return launch_kind<Q4KV_Q8, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, nullptr, pb);
     /* other widths and shapes: the append launch, then the attention */
     const uint32_t row = kv_f16 == Q4KV_Q8 ? hd / 32u * 34u : hd * (kv_f16 == Q4KV_F16 ? 2u : 4u);
     if (!q4kv_append_steps(d_descs, n_seq, n_kvh * hd, n_kvh * row, kv_f16)) return false;
-    return launch_attn<MODE_BATCH>(kv_f16, a, n_seq * n_kvh, max_n);
+    return launch_attn<MODE_BATCH>(kv_f16, a, n_seq * n_kvh, max_n, pb);
+}
+
+extern "C" bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq,
+                                      uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
+                                      int kv_f16, uint32_t max_n) {
+    if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
+        return false;
+    return step_batch(d_descs, n_seq, n_head, n_kvh, hd, scale, kv_f16, max_n, lib_part());
+}
+
+/* ---- the no-allocation variant of q4_hip_qsa_step_batch ----
+ * Its split partials live in this file-scope device array instead of the
+ * buffer q4_hip_init allocates. Each device holds its own copy; the host
+ * reaches it only through the address hipGetSymbolAddress returns for the
+ * current device (the array's name in host code is not a device address).
+ * Nothing in it needs clearing: every partial row the merge reads is
+ * written by the same launch first. Calls that overlap on one device share
+ * the array and race. */
+#define Q4KV_SCRATCH_FLOATS (4u << 20) /* 16 MiB */
+#define Q4KV_SCRATCH_DEVS 64
+static __device__ __align__(256) float scratch[Q4KV_SCRATCH_FLOATS];
+static float *g_scratch_ptr[Q4KV_SCRATCH_DEVS];
+
+/* Resolve the scratch address on the current device (once per device; the
+ * library's init calls it with its device current). */
+extern "C" bool q4kv_scratch_init(void) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= Q4KV_SCRATCH_DEVS) {
+        (void)hipGetLastError();
+        Q4KV_ERR("scratch init: no current device below %d", Q4KV_SCRATCH_DEVS);
+        return false;
+    }
+    if (g_scratch_ptr[dev]) return true;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        Q4KV_ERR("scratch init: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        return false;
+    }
+    g_scratch_ptr[dev] = (float *)p;
+    return true;
+}
+
+extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uint32_t n_seq,
+                                              uint32_t n_head, uint32_t n_kvh, uint32_t hd,
+                                              float scale, int kv_f16, uint32_t max_n) {
+    if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
+        return false;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= Q4KV_SCRATCH_DEVS ||
+        !g_scratch_ptr[dev]) {
+        (void)hipGetLastError();
+        Q4KV_ERR("qsa_step_batch_noalloc: scratch not resolved on this device (q4_hip_init)");
+        return false;
+    }
+    /* the same split division as q4_hip_qsa_step_batch (so the same results),
+     * which must fit the static scratch */
+    const uint32_t gqa = n_head / n_kvh, n_items = n_seq * n_kvh;
+    const uint32_t cp = kv_f16 == Q4KV_F32 ? KCfg<Q4KV_F32>::CP : KCfg<Q4KV_Q8>::CP;
+    uint32_t S, cps;
+    choose_split(n_items, (max_n + cp - 1u) / cp, gqa, q4kv_part != nullptr, q4kv_part_cap, S,
+                 cps);
+    const size_t need = S > 1u ? (size_t)n_items * S * gqa * PSTRIDE : 0u;
+    if (need > Q4KV_SCRATCH_FLOATS) {
+        Q4KV_ERR("qsa_step_batch_noalloc: %u items x %u splits need %zu floats of scratch, "
+                 "the maximum is %u",
+                 n_items, S, need, Q4KV_SCRATCH_FLOATS);
+        return false;
+    }
+    return step_batch(d_descs, n_seq, n_head, n_kvh, hd, scale, kv_f16, max_n,
+                      PartBuf{g_scratch_ptr[dev], q4kv_part_cap});
 }
 
 #ifdef Q4KV_TRACE

@@ -21,6 +21,10 @@ extern int32_t *q4kv_pos_d;
 extern float *q4kv_part;
 extern size_t q4kv_part_cap;
 
+/* Resolves the no-allocation entry point's static scratch on the current
+ * device (q4kv_attn.hip); q4_hip_init calls it once. */
+extern "C" bool q4kv_scratch_init(void);
+
 /* The append half of q4_hip_qsa_step_batch for widths the fused kernel
  * does not cover: d_step_descs is a device array of q4kv_step_desc. */
 bool q4kv_append_steps(const void *d_step_descs, uint32_t n_desc, uint32_t n, uint32_t bpt,

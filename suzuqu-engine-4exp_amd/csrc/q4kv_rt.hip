@@ -89,6 +89,7 @@ extern "C" bool q4_hip_init(void) {
         q4kv_part = nullptr;
         q4kv_part_cap = 0;
     }
+    if (!q4kv_scratch_init()) return false;
     q4kv_ok = 1;
     return true;
 }

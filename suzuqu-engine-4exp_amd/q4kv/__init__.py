@@ -156,6 +156,7 @@ SIGNATURES = {
                                       _u32, _u32, _u32, _u32, _f32, C.c_int]),
     "q4_hip_qsa_decode_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32]),
     "q4_hip_qsa_step_batch": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32]),
+    "q4_hip_qsa_step_batch_noalloc": (_b, [_vp, _u32, _u32, _u32, _u32, _f32, C.c_int, _u32]),
     "q4_hip_host_alloc": (_vp, [C.c_size_t]),
     "q4_hip_host_free": (None, [_vp]),
     "q4kv_timer_begin": (_b, [C.c_int]),
