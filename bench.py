@@ -717,6 +717,40 @@ def config_out(b, steps=100, sets=4, n_embd=4096):
     return out
 
 
+def config_gqa12(b, steps=200, n_head=24):
+    """The reference's production head layout (24 query heads over 2 KV heads,
+    12 per KV head; SURVEY's model shape) on config 1's 12-layer decode step:
+    q8_0 append + sparse attention over the same caches and selections,
+    through q4_hip_qsa_step_batch (one fused launch + the merge)."""
+    rt, lib = b.rt, b.lib
+    L, R = b.L, b.R
+    qb = n_head * HD * 4
+    dq = rt.alloc(R * L * qb)
+    b.gen(dq, R * L * n_head * HD, 95)
+    dout = rt.alloc(L * qb)
+    steps_d = (q4kv.StepDesc * (R * L))()
+    for r in range(R):
+        for li in range(L):
+            i = r * L + li
+            seq = q4kv.SeqDesc(b.kc[li], b.vc[li], dq + i * qb, None, dout + li * qb,
+                               b.sel_ptr(r, li), WIDTH, WIDTH, CTX, 0)
+            steps_d[i] = q4kv.StepDesc(seq, b.row_ptr(b.d_nk, r, li), b.row_ptr(b.d_nv, r, li),
+                                       b.pos[r])
+    dd = rt.alloc(C.sizeof(steps_d))
+    assert lib.q4_hip_h2d(dd, C.addressof(steps_d), C.sizeof(steps_d))
+    sz = C.sizeof(q4kv.StepDesc)
+    t, t_graph = _time_both(b, lambda r: lib.q4_hip_qsa_step_batch(
+        dd + r * L * sz, L, n_head, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH), R, steps)
+    byts = GATHER_B + IDX_B + 2 * qb + APPEND_B
+    for p_ in (dq, dout, dd):
+        rt.free(p_)
+    return {"what": f"{L}-layer decode step, {n_head} query heads / {N_KVH} KV heads "
+                    f"(gqa {n_head // N_KVH}), same caches and selections as the headline",
+            "us_per_layer": round(t / L * 1e6, 3), "graph_us_per_layer": round(t_graph / L * 1e6, 3),
+            "bytes_per_layer": byts, "gbs": round(byts * L / t / 1e9, 1),
+            "selection_sets": R}
+
+
 IDX_RATIO, IDX_KBLK, IDX_HEADS, IDX_DIM = 4, 512, 4, 128
 IDX_ROT, IDX_BASE, IDX_EPS = 64, 1.0e7, 1.0e-6
 
@@ -881,6 +915,7 @@ def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
 
 
 ONLY = {"config2": config2, "config3": config3, "config4": config4, "prep": config_prep,
+        "gqa12": config_gqa12,
         "out": config_out, "indexer": config_indexer,
         "indexer_prefill": config_indexer_prefill}
 
@@ -944,6 +979,7 @@ def main():
     if args.configs:
         configs = {"config2_batched_decode": config2(b), "config3_chunked_prefill": config3(b),
                    "config4_widths_restore": config4(b),
+                   "production_heads_24_2": config_gqa12(b),
                    "qk_prep_fused_step": config_prep(b),
                    "out_projection_fused": config_out(b),
                    "indexer_decode": config_indexer(b),

@@ -263,8 +263,15 @@ __device__ uint64_t q4kv_trace_buf[4096 * 16];
             q4kv_trace_buf[((blockIdx.y * gridDim.x + blockIdx.x) & 4095u) * 16u + (slot)] = \
                 wall_clock64();                                                    \
     } while (0)
+#define TRACEW(slot)                                                                   \
+    do {                                                                               \
+        if ((threadIdx.x & 63u) == 0)                                                  \
+            q4kv_trace_buf[((((blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x >> 6)) + (threadIdx.x >> 6)) & \
+                            4095u) * 16u + (slot)] = wall_clock64();                   \
+    } while (0)
 #else
 #define TRACE(slot) do { } while (0)
+#define TRACEW(slot) do { } while (0)
 #endif
 
 template <int KIND> struct KCfg;
@@ -1213,6 +1220,502 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     TRACE(12);
 }
 
+/* ------------------------------------------------------------------------
+ * Slab kernel: the q8_0 / head_dim 256 decode path for up to 16 query heads
+ * per KV head. One wave owns a slab of 32 list entries and computes it end to
+ * end (Q.K, softmax, P.V) with no workgroup barrier; the workgroup's waves
+ * merge their (m, l, acc) once at the end. Every wave issues its slab's
+ * index load and K/V row DMAs first, so all of a workgroup's rows are in
+ * flight together; the workgroup builds the Q operands in LDS meanwhile.
+ *
+ * Per wave, in S^T = K.Q^T form (MFMA v_mfma_f32_16x16x32_f16):
+ *  - A = K rows (16 positions x 32 dims of one q8_0 block, int8 -> fp16 via
+ *    the exponent trick: 1152 + k), B = Q^T for 16 columns: columns 0-7 the
+ *    fp16 part (truncated) of 8 query heads' q, pre-scaled to log2 units,
+ *    columns 8-15 the fp16 residual, so a score is column c plus column c + 8.
+ *  - The +1152 bias and the per-position q8_0 scales: S = sum_b ks[p][b] C_b
+ *    + C', where one more MFMA gives C'[p][c] = sum_b ks[p][b] qbias[b][c]
+ *    with qbias = -1152 sum_k q split into three fp16 parts (K slots 0-23),
+ *    and slot 24 carries -65504 for list entries that are padding.
+ *  - A lane's C rows (4 positions of each 16-position tile) are exactly the
+ *    8 K slots its P.V B operand needs, so the softmax weights never leave
+ *    the lane: P.V runs as O^T = V^T.P^T with B = the weights times the V
+ *    block scale, split hi (columns 0-7) / lo (8-15), and A = V^T gathered
+ *    with 16-bit LDS reads (two adjacent dims feed an even-dim and an odd-dim
+ *    tile). The V bias leaves through one MFMA with a -1152 operand per tile.
+ * ------------------------------------------------------------------------ */
+constexpr uint32_t SLAB = 32;
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+/* K operand of block b, k-group jg from a raw q8_0 row in LDS, biased
+ * (1152 + k), in q8_kdim order. */
+__device__ static inline h8_t k_operand_biased(const uint8_t *row, uint32_t b, uint32_t jg,
+                                               uint32_t k_eoff, uint32_t k_esel) {
+    const uint8_t *pb = row + 68u * (b >> 1);
+    uint32_t w0, w1;
+    if (b & 1u) {
+        w0 = *(const uint32_t *)(pb + 36u + 8u * jg);
+        w1 = *(const uint32_t *)(pb + 40u + 8u * jg);
+    } else {
+        w0 = *(const uint32_t *)(pb + k_eoff);
+        w1 = __builtin_amdgcn_perm(*(const uint32_t *)(pb + k_eoff + 4u), *(const uint32_t *)pb,
+                                   k_esel);
+    }
+    uint32_t r0, r1, r2, r3;
+    i8x4_to_h4(w0, r0, r1);
+    i8x4_to_h4(w1, r2, r3);
+    return __builtin_bit_cast(h8_t, (u4_t){r0, r1, r2, r3});
+}
+
+/* Reductions across the four 16-lane rows (v_permlane16_swap: the lane 16
+ * apart within each half; v_permlane32_swap: the lane 32 apart). */
+__device__ static inline float sum16(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ static inline float max16(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ static inline float max32(float v) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+/* v + (value of lane c + 8 mod 16 in the same DPP row): hi + lo columns */
+__device__ static inline float add_ror8(float v) {
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+}
+/* fp16 halves of a packed word as fp32 (folded into v_fma_mix operands) */
+__device__ static inline float h2lo(uint32_t w) { return (float)__builtin_bit_cast(h2_t, w)[0]; }
+__device__ static inline float h2hi(uint32_t w) { return (float)__builtin_bit_cast(h2_t, w)[1]; }
+/* x, y -> two fp16 by truncation, packed (v_cvt_pkrtz_f16_f32) */
+__device__ static inline uint32_t pkrtz(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x, y));
+}
+/* fp16 hi part of (x, y) (nsel = 0) or the fp16 residual x - hi (nsel = -1),
+ * packed; hi by truncation, so hi + lo carries ~21 bits. */
+__device__ static inline uint32_t split_pk(float x, float y, float nsel) {
+    const uint32_t h = pkrtz(x, y);
+    return pkrtz(__builtin_fmaf(nsel, h2lo(h), x), __builtin_fmaf(nsel, h2hi(h), y));
+}
+/* an fp16 in LDS as fp32 (folded into v_fma_mix operands) */
+__device__ static inline float ld_h(const uint8_t *p) {
+    return (float)__builtin_bit_cast(_Float16, *(const uint16_t *)p);
+}
+/* two 16-bit LDS values packed into one word */
+__device__ static inline uint32_t lds_u16x2(const uint8_t *a, const uint8_t *b) {
+    return (uint32_t)*(const uint16_t *)a | ((uint32_t)*(const uint16_t *)b << 16);
+}
+
+template <int MODE, int HG>
+__global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
+    constexpr uint32_t ROWB = 272, NCH = 17;
+    constexpr uint32_t NSLAB = 4u / HG, NE = NSLAB * SLAB; /* slabs, entries per pass */
+    constexpr uint32_t RBYTES = 2u * NE * ROWB;           /* K rows | V rows */
+    constexpr uint32_t MBYTES = 4u * 16u * 8u * 20u * 4u;  /* merge: [wave][tile][head][20] */
+    __shared__ __attribute__((aligned(16))) uint8_t rows[RBYTES > MBYTES ? RBYTES : MBYTES];
+    /* Q^T operands [head group][block][k-group][column][8 fp16] and the bias
+     * operand [head group][k-group][column][8 fp16] */
+    __shared__ __attribute__((aligned(16))) uint16_t qB[HG][8][4][16][8];
+    __shared__ __attribute__((aligned(16))) uint16_t qbB[HG][4][16][8];
+    /* V block scales of each slab, block-major (fp16 bits, 0 at padding) */
+    __shared__ __attribute__((aligned(16))) uint16_t vsT[NSLAB][8][SLAB];
+    __shared__ int32_t s_pos[NE];
+    __shared__ float s_m[4][8], s_l[4][8];
+    /* MODE_PSTEP: the prepared query rows and the prepared new key row */
+    constexpr bool PREP = MODE == MODE_PSTEP;
+    __shared__ __attribute__((aligned(16))) float qst[PREP ? 8u * HG : 1u][PREP ? 256u : 1u];
+    __shared__ __attribute__((aligned(16))) float kst[PREP ? 256u : 1u];
+
+    TRACEW(0);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t slab = wave / HG, hg = wave % HG;
+    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
+    const Item it = resolve_item<MODE>(a, item);
+    const uint32_t c = lane & 15u, jg = lane >> 4; /* MFMA column / row, k-group */
+    const float nsel = c >= 8u ? -1.f : 0.f;
+    const size_t rstride = (size_t)a.n_kvh * ROWB;
+    const uint8_t *kbase = it.kc + (size_t)kh * ROWB, *vbase = it.vc + (size_t)kh * ROWB;
+    const uint32_t k_eoff = jg < 3u ? 4u + 8u * jg : 28u;
+    const uint32_t k_esel = jg == 3u ? 0x05040302u : 0x07060504u;
+    uint8_t *const krow = rows + slab * SLAB * ROWB;
+    uint8_t *const vrow = rows + NE * ROWB + slab * SLAB * ROWB;
+    const uint32_t n = it.n;
+    const uint32_t j0 = (uint32_t)(((uint64_t)s * n) / a.S);
+    const uint32_t j1 = (uint32_t)(((uint64_t)(s + 1u) * n) / a.S);
+    /* passes: every wave of the workgroup runs the same number (barriers
+     * stay matched); pass k covers entries j0 + k * NE + slab * 32 .. + 31 */
+    const uint32_t n_pass = j1 > j0 ? (j1 - j0 + NE - 1u) / NE : 0u;
+
+    int32_t raw = -1;
+    {
+        const uint32_t e = j0 + slab * SLAB + (lane & 31u);
+        if (e < j1) raw = it.list ? ldg(it.list + e) : (int32_t)e;
+    }
+    /* MODE_STEP: every lane holds four fp32 of the token's K row and four of
+     * its V row (lane l: block l >> 3, part l & 7); split 0's wave 0 writes
+     * the quantised rows to the caches, and a wave whose slab lists the
+     * position uses the same bytes in LDS instead of the fetched row. */
+    float nk[4] = {0.f, 0.f, 0.f, 0.f}, nv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (IS_STEP(MODE)) {
+        const uint32_t off = 32u * (lane >> 3) + 4u * (lane & 7u);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            nk[i] = ldg(it.knew + off + i);
+            nv[i] = ldg(it.vnew + off + i);
+        }
+    }
+    /* this thread's share of the Q operands: head slot hh of head group k,
+     * block b, k-group kg (8 dims in q8_kdim order); loaded here so the loads
+     * overlap the DMA issue (with the prep: after it, from the prepared rows) */
+    float qx[HG][8];
+    const uint32_t t_kg = tid & 3u, t_b = (tid >> 2) & 7u, t_hh = tid >> 5;
+    auto load_qx = [&]() {
+#pragma unroll
+        for (uint32_t k = 0; k < HG; k++) {
+            const uint32_t h = 8u * k + t_hh;
+            const float *qr = PREP ? &qst[h < gqa ? h : 0u][32u * t_b]
+                                   : it.q + (size_t)(h < gqa ? h : 0u) * 256u + 32u * t_b;
+#pragma unroll
+            for (uint32_t kk = 0; kk < 4u; kk++) {
+                const fv2 v = PREP ? *(const fv2 *)(qr + q8_kdim(t_b, t_kg, 2u * kk))
+                                   : ldg((const fv2 *)(qr + q8_kdim(t_b, t_kg, 2u * kk)));
+                qx[k][2u * kk] = h < gqa ? v[0] * a.scale_log2 : 0.f;
+                qx[k][2u * kk + 1u] = h < gqa ? v[1] * a.scale_log2 : 0.f;
+            }
+        }
+    };
+    if (!PREP) load_qx();
+
+    /* issue pass p: positions into s_pos, the slab's K/V rows by DMA (32 x
+     * 17 sixteen-byte pieces per cache, piece u * 64 + lane, row = piece /
+     * 17); returns whether the slab holds any valid position */
+    auto issue = [&](uint32_t pass, uint32_t &ne, int32_t &pos) -> bool {
+        const uint32_t e0 = j0 + pass * NE + slab * SLAB;
+        ne = e0 < j1 ? min(SLAB, j1 - e0) : 0u;
+        pos = (raw >= 0 && (uint32_t)raw < it.max_kv && (lane & 31u) < ne) ? raw : -1;
+        const bool any = __ballot(pos >= 0) != 0u;
+        if (lane < 32u && hg == 0u) s_pos[slab * SLAB + lane] = pos;
+        if (hg == 0u && any) {
+#pragma unroll
+            for (uint32_t u = 0; u < 9u; u++) {
+                const uint32_t e = u * 64u + lane;
+                const uint32_t r = e / NCH, q = e - r * NCH;
+                const int32_t pr = __builtin_amdgcn_ds_bpermute((int)((r & 31u) * 4u), pos);
+                const size_t off = (size_t)(pr < 0 ? 0 : pr) * rstride + q * 16u;
+                if (u < 8u || lane < 32u) {
+                    dma16(kbase + off, krow + u * 1024u);
+                    dma16(vbase + off, vrow + u * 1024u);
+                }
+            }
+        }
+        return any;
+    };
+    uint32_t ne = 0;
+    int32_t pos = -1;
+    bool any = n_pass > 0u ? issue(0u, ne, pos) : false;
+    TRACEW(1);
+
+    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
+        int q[4];
+        float d;
+        uint8_t *row;
+        if (!PREP) { /* with the prep the K row is written once prepared */
+            d = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
+            row = (uint8_t *)kbase + (size_t)it.pos_new * rstride;
+            q8_lane_store(row + 34u * (lane >> 3), lane & 7u, d, q);
+        }
+        d = q8_lane_quant(nv[0], nv[1], nv[2], nv[3], q);
+        row = (uint8_t *)vbase + (size_t)it.pos_new * rstride;
+        q8_lane_store(row + 34u * (lane >> 3), lane & 7u, d, q);
+    }
+
+    if (PREP) {
+        /* RMSNorm + RoPE of the query heads (wave w: heads w, w + 4, ..) and,
+         * by wave 0, of the new key row, at the token's position, through the
+         * routine the separate prep entry points use; split 0 copies the gate
+         * halves of the [q | gate] rows to the gate buffer the merge reads */
+        for (uint32_t h = wave; h < gqa; h += 4u)
+            q4kv_prep_row(it.q + (size_t)h * 512u, qst[h], it.wnq, 256u, a.n_rot,
+                          (int32_t)it.pos_new, a.rope_base, a.eps, lane);
+        if (wave == 0u)
+            q4kv_prep_row(it.knew, kst, it.wnk, 256u, a.n_rot, (int32_t)it.pos_new, a.rope_base,
+                          a.eps, lane);
+        if (s == 0u && it.gate) {
+            for (uint32_t e = tid; e < gqa * 64u; e += 256u) {
+                const uint32_t h = e >> 6, d = (e & 63u) * 4u;
+                *(float4 *)((float *)it.gate + (size_t)h * 256u + d) =
+                    *(const float4 *)(it.q + (size_t)h * 512u + 256u + d);
+            }
+        }
+        __syncthreads();
+        load_qx();
+        const uint32_t off = 32u * (lane >> 3) + 4u * (lane & 7u);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) nk[i] = kst[off + i];
+        if (s == 0u && wave == 0u && it.pos_new < it.max_kv) {
+            int q[4];
+            const float d = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
+            uint8_t *row = (uint8_t *)kbase + (size_t)it.pos_new * rstride;
+            q8_lane_store(row + 34u * (lane >> 3), lane & 7u, d, q);
+        }
+    }
+
+    /* ---- Q^T operands and the bias operand, built once per workgroup ---- */
+#pragma unroll
+    for (uint32_t k = 0; k < HG; k++) {
+        uint32_t hw[4], lw[4];
+        float sh = 0.f, sl = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            hw[i] = pkrtz(qx[k][2u * i], qx[k][2u * i + 1u]);
+            lw[i] = pkrtz(qx[k][2u * i] - h2lo(hw[i]), qx[k][2u * i + 1u] - h2hi(hw[i]));
+            sh += h2lo(hw[i]) + h2hi(hw[i]);
+            sl += h2lo(lw[i]) + h2hi(lw[i]);
+        }
+        *(u4_t *)&qB[k][t_b][t_kg][t_hh][0] = (u4_t){hw[0], hw[1], hw[2], hw[3]};
+        *(u4_t *)&qB[k][t_b][t_kg][t_hh + 8u][0] = (u4_t){lw[0], lw[1], lw[2], lw[3]};
+        /* the block's column sums: the four k-groups are a lane quad */
+        sh += dppf<0xB1>(sh);
+        sh += dppf<0x4E>(sh);
+        sl += dppf<0xB1>(sl);
+        sl += dppf<0x4E>(sl);
+        if (t_kg == 0u) {
+#pragma unroll
+            for (uint32_t lo = 0; lo < 2u; lo++) {
+                const float x = -1152.f * (lo ? sl : sh);
+                const _Float16 p1 = (_Float16)x;
+                const float r1 = x - (float)p1;
+                const _Float16 p2 = (_Float16)r1;
+                const _Float16 p3 = (_Float16)(r1 - (float)p2);
+                const uint32_t col = t_hh + 8u * lo;
+                qbB[k][0][col][t_b] = __builtin_bit_cast(uint16_t, p1);
+                qbB[k][1][col][t_b] = __builtin_bit_cast(uint16_t, p2);
+                qbB[k][2][col][t_b] = __builtin_bit_cast(uint16_t, p3);
+            }
+        }
+        if (tid < 16u) /* slot 24: the padding penalty (fp16 -65504) */
+            *(u4_t *)&qbB[k][3][tid][0] = (u4_t){0xFBFFu, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    TRACEW(2);
+
+    float m_run = -INFINITY, l_run = 0.f;
+    f4_t acc[16];
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; t++) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    const h8_t neg = (h8_t)((_Float16)-1152.0f);
+    const uint16_t *const qBw = &qB[hg][0][jg][c][0];
+    const h8_t qbias_op = *(const h8_t *)&qbB[hg][jg][c][0];
+
+    for (uint32_t pass = 0; pass < n_pass; pass++) {
+        if (pass > 0u) any = issue(pass, ne, pos);
+        /* the next pass's list entries (a wave rarely has more than one) */
+        raw = -1;
+        {
+            const uint32_t e = j0 + (pass + 1u) * NE + slab * SLAB + (lane & 31u);
+            if (pass + 1u < n_pass && e < j1) raw = it.list ? ldg(it.list + e) : (int32_t)e;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        TRACEW(3);
+        if (HG > 1) __syncthreads(); /* the head-group waves share the slab's rows */
+        if (hg == 0u && any) {
+            if (IS_STEP(MODE)) {
+                /* rows at the appended position take the new token's bytes */
+                uint64_t hit = __ballot(lane < 32u && pos >= 0 && (uint32_t)pos == it.pos_new);
+                if (hit) {
+                    int q[4], qv[4];
+                    const float dk = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
+                    const float dv = q8_lane_quant(nv[0], nv[1], nv[2], nv[3], qv);
+                    while (hit) {
+                        const uint32_t r = __builtin_ctzll(hit);
+                        hit &= hit - 1u;
+                        q8_lane_store(krow + r * ROWB + 34u * (lane >> 3), lane & 7u, dk, q);
+                        q8_lane_store(vrow + r * ROWB + 34u * (lane >> 3), lane & 7u, dv, qv);
+                    }
+                }
+            }
+            /* padding rows (never fetched, or fetched from row 0): zero their
+             * K block scales; the V block scales go block-major to vsT, 0 at
+             * padding */
+            if (lane < 32u && pos < 0) {
+#pragma unroll
+                for (uint32_t b = 0; b < 8u; b++) *(uint16_t *)(krow + lane * ROWB + 34u * b) = 0;
+            }
+            {
+                const uint32_t p = lane & 31u;
+                const bool valid = s_pos[slab * SLAB + p] >= 0;
+#pragma unroll
+                for (uint32_t k = 0; k < 4u; k++) {
+                    const uint32_t b = (lane >> 5) + 2u * k;
+                    vsT[slab][b][p] = valid ? *(const uint16_t *)(vrow + p * ROWB + 34u * b) : 0;
+                }
+            }
+        }
+        if (HG > 1) __syncthreads();
+        if (any) {
+            TRACEW(4);
+            /* ---- scores: two 16-position tiles ---- */
+            f4_t S[2];
+#pragma unroll
+            for (uint32_t t = 0; t < 2u; t++) {
+                /* A' row p = 16 t + c: the 8 K scales (k-groups 0-2), or the
+                 * padding flag (k-group 3) */
+                const uint8_t *rp = krow + (16u * t + c) * ROWB;
+                u4_t w;
+#pragma unroll
+                for (uint32_t i = 0; i < 4u; i++) w[i] = lds_u16x2(rp + 68u * i, rp + 68u * i + 34u);
+                const bool pad = s_pos[slab * SLAB + 16u * t + c] < 0;
+                const u4_t wf = {pad ? 0x3C00u : 0u, 0u, 0u, 0u};
+                const u4_t ap = jg == 3u ? wf : w;
+                S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, ap),
+                                                              qbias_op,
+                                                              (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            }
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++) {
+                const h8_t qb = *(const h8_t *)(qBw + b * 4u * 16u * 8u);
+#pragma unroll
+                for (uint32_t t = 0; t < 2u; t++) {
+                    const h8_t kb =
+                        k_operand_biased(krow + (16u * t + c) * ROWB, b, jg, k_eoff, k_esel);
+                    const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        kb, qb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const uint8_t *rs = krow + (16u * t + 4u * jg) * ROWB + 34u * b;
+#pragma unroll
+                    for (uint32_t i = 0; i < 4u; i++)
+                        S[t][i] = __builtin_fmaf(ld_h(rs + i * ROWB), C[i], S[t][i]);
+                }
+            }
+            TRACEW(5);
+            /* ---- softmax over the slab (base 2; scores already scaled) ---- */
+            float T[8];
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                T[i] = add_ror8(S[0][i]);
+                T[4u + i] = add_ror8(S[1][i]);
+            }
+            float mx = fmax3v(fmax3v(T[0], T[1], T[2]), fmax3v(T[3], T[4], T[5]), fmax2(T[6], T[7]));
+            mx = max32(max16(mx));
+            const float mn = fmax2(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+            m_run = mn;
+            float P[8], ls = 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < 8u; i++) {
+                P[i] = __builtin_amdgcn_exp2f(T[i] - mn);
+                ls += P[i];
+            }
+            l_run = l_run * alpha + ls;
+            if (pass > 0u) {
+#pragma unroll
+                for (uint32_t t = 0; t < 16u; t++) acc[t] *= alpha;
+            }
+            TRACEW(6);
+            /* ---- P.V over the 8 blocks: tiles 2b (even dims), 2b + 1 (odd) ---- */
+            /* this lane's 8 positions: 4 jg .. 4 jg + 3, 16 + 4 jg .. 16 + 4 jg + 3 */
+            const uint8_t *vp0 = vrow + (4u * jg) * ROWB, *vp1 = vrow + (16u + 4u * jg) * ROWB;
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++) {
+                const uint8_t *s0 = vp0 + 34u * b, *s1 = vp1 + 34u * b;
+                const uint2 va = *(const uint2 *)&vsT[slab][b][4u * jg];
+                const uint2 vb = *(const uint2 *)&vsT[slab][b][16u + 4u * jg];
+                const uint32_t vw[4] = {va.x, va.y, vb.x, vb.y};
+                float u[8];
+#pragma unroll
+                for (uint32_t i = 0; i < 4u; i++) {
+                    u[2u * i] = __builtin_fmaf(P[2u * i], h2lo(vw[i]), 0.f);
+                    u[2u * i + 1u] = __builtin_fmaf(P[2u * i + 1u], h2hi(vw[i]), 0.f);
+                }
+                const u4_t bw = {split_pk(u[0], u[1], nsel), split_pk(u[2], u[3], nsel),
+                                 split_pk(u[4], u[5], nsel), split_pk(u[6], u[7], nsel)};
+                const h8_t B = __builtin_bit_cast(h8_t, bw);
+                /* V^T: dims 2c, 2c + 1 of block b at the lane's 8 positions */
+                u4_t E, O;
+#pragma unroll
+                for (uint32_t k = 0; k < 4u; k++) {
+                    const uint8_t *vd = (k < 2u ? s0 : s1) + 2u + 2u * c + (2u * (k & 1u)) * ROWB;
+                    uint32_t x = lds_u16x2(vd, vd + ROWB);
+                    x ^= 0x80808080u;
+                    E[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04020400u);
+                    O[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04030401u);
+                }
+                acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(h8_t, E), B, acc[2u * b], 0, 0, 0);
+                acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b], 0, 0, 0);
+                acc[2u * b + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(h8_t, O), B, acc[2u * b + 1u], 0, 0, 0);
+                acc[2u * b + 1u] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b + 1u], 0, 0, 0);
+            }
+        }
+        if (HG > 1) __syncthreads(); /* the slab's rows are refilled next pass */
+    }
+    TRACEW(7);
+
+    /* ---- merge the waves: (m, l) per head, acc to the common max ---- */
+    const float lw = pair32_sum(sum16(l_run));
+    if (lane < 8u) {
+        s_m[wave][lane] = m_run;
+        s_l[wave][lane] = lw;
+    }
+    __syncthreads(); /* every wave is done with the rows: the merge reuses them */
+    TRACEW(8);
+    float *const mrg = (float *)rows;
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; t++) {
+        f4_t v;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) v[i] = add_ror8(acc[t][i]);
+        if (c < 8u) *(f4_t *)(mrg + ((wave * 16u + t) * 8u + c) * 20u + 4u * jg) = v;
+    }
+    __syncthreads();
+    TRACEW(9);
+#pragma unroll
+    for (uint32_t k = 0; k < 2u * HG; k++) {
+        const uint32_t task = tid + 256u * k;
+        const uint32_t thg = task >> 9, hh = (task >> 6) & 7u, t = (task >> 2) & 15u, jq = task & 3u;
+        const uint32_t g = 8u * thg + hh;
+        if (g >= gqa) continue;
+        float Mh = -INFINITY;
+#pragma unroll
+        for (uint32_t w = thg; w < 4u; w += HG) Mh = fmax2(Mh, s_m[w][hh]);
+        float L = 0.f;
+        f4_t v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t w = thg; w < 4u; w += HG) {
+            const float mw = s_m[w][hh];
+            const float fw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - Mh);
+            L += fw * s_l[w][hh];
+            v += fw * *(const f4_t *)(mrg + ((w * 16u + t) * 8u + hh) * 20u + 4u * jq);
+        }
+        const uint32_t col = 16u * t + 4u * jq;
+        if (a.S == 1u) {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                const uint32_t d = col_dim<Q4KV_Q8>(col + i);
+                float r = v[i] * inv;
+                if (it.gate) {
+                    /* with the prep: the gate half of the source row (the copy
+                     * above is for the merge kernel) */
+                    const float gv = PREP ? ldg(it.q + (size_t)g * 512u + 256u + d)
+                                          : ldg(it.gate + (size_t)g * 256u + d);
+                    r *= 1.f / (1.f + expf(-gv));
+                }
+                stg(it.out + (size_t)g * 256u + d, r);
+            }
+        } else {
+            float *pb = a.part + ((size_t)item * a.S + s) * gqa * PSTRIDE + (size_t)g * PSTRIDE;
+            stg((fv2 *)(pb + 2u + col), (fv2){v[0], v[1]});
+            stg((fv2 *)(pb + 4u + col), (fv2){v[2], v[3]});
+            if (t == 0u && jq == 0u) stg((fv2 *)pb, (fv2){Mh, L});
+        }
+    }
+    TRACEW(10);
+}
+
 /* Merge the S split partials of one (item, head): weights 2^(m_s - M) over
  * splits with l_s > 0, then the sigmoid gate (src/q4_rocm.cu:6968-7013).
  * Thread c owns output column c. For S <= COMB_REG every partial load
@@ -1430,6 +1933,18 @@ static uint32_t split_target(void) {
 }
 #define Q4KV_MAX_GRID_Y 65535u
 
+/* Chunks per workgroup from which the fast kernel double-buffers its rows
+ * (Q4KV_DB_MIN overrides, for measurement). */
+static uint32_t db_min_chunks(void) {
+    static uint32_t t = 0;
+    if (!t) {
+        const char *e = getenv("Q4KV_DB_MIN");
+        const long v = e ? strtol(e, nullptr, 10) : 0;
+        t = (v >= 1 && v <= 1 << 20) ? (uint32_t)v : 3u;
+    }
+    return t;
+}
+
 struct OutProj {
     const q4kv_out_desc *od;
     uint32_t n_embd;
@@ -1465,15 +1980,70 @@ static void choose_split(uint32_t n_items, uint32_t n_chunks, uint32_t gqa, bool
     if (S < 1u) S = 1u;
 }
 
+/* Which kernel runs a launch, and its split division. */
+struct Plan {
+    bool slab;    /* qsa_slab_k (else qsa_q8d256_k / qsa_attn_k) */
+    uint32_t hg;  /* slab kernel: head groups of 8 */
+    uint32_t S, cps;
+};
+
+/* The slab kernel takes q8_0 / hd 256 decode shapes with 9 to 16 query heads
+ * per KV head (two head groups; up to 8 heads the chunk kernel qsa_q8d256_k
+ * measures faster), while the launch stays small enough that its splits of
+ * 64 list entries keep the chip busy without a flood of partials;
+ * prefill-sized launches keep the chunk-streaming kernel. Q4KV_SLAB=0 turns
+ * it off, Q4KV_SLAB=2 uses it from one head up (A/B measurement). */
+#define SLAB_MAX_WG 16384u
+static int slab_mode(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_SLAB");
+        v = !e ? 1 : e[0] == '0' ? 0 : e[0] == '2' ? 2 : 1;
+    }
+    return v;
+}
+static bool slab_takes(uint32_t gqa) {
+    const int m = slab_mode();
+    return gqa <= 16u && (m == 2 || (m == 1 && gqa > 8u));
+}
+
+template <int KIND, int MODE>
+static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t gqa,
+                        bool have_part, size_t cap) {
+    Plan pl = {false, 1u, 1u, 1u};
+    if (KIND == Q4KV_Q8 && hd == 256u && slab_takes(gqa)) {
+        const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
+        uint32_t S = (max_n + ne - 1u) / ne;
+        if (S < 1u) S = 1u;
+        if ((uint64_t)n_items * S <= SLAB_MAX_WG) {
+            if (S > COMB_MAXS) S = COMB_MAXS;
+            const size_t per = (size_t)gqa * PSTRIDE;
+            while (S > 1u && (size_t)n_items * S * per > cap) S--; /* waves then loop */
+            if (!have_part) S = 1u;
+            pl.slab = true;
+            pl.hg = hg;
+            pl.S = S;
+            pl.cps = 0u;
+            return pl;
+        }
+    }
+    constexpr uint32_t CP = KCfg<KIND>::CP;
+    choose_split(n_items, (max_n + CP - 1u) / CP, gqa, have_part, cap, pl.S, pl.cps);
+    return pl;
+}
+
+/* A fused append + attention launch exists for this shape. */
+static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
+    return kind == Q4KV_Q8 && hd == 256u && (gqa <= 8u || slab_takes(gqa));
+}
+
 template <int KIND, int MODE>
 static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa,
                         const OutProj *op = nullptr, PartBuf pb = lib_part()) {
-    constexpr uint32_t CP = KCfg<KIND>::CP;
-    const uint32_t n_chunks = (max_n + CP - 1u) / CP;
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
-    if (IS_STEP(MODE) && !fast) return false; /* the fused append needs the fast kernel */
-    uint32_t S, cps;
-    choose_split(n_items, n_chunks, gqa, pb.ptr != nullptr, pb.cap, S, cps);
+    const Plan pl = plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap);
+    if (IS_STEP(MODE) && !fast && !pl.slab) return false; /* the fused append needs these */
+    const uint32_t S = pl.S, cps = pl.cps;
     a.S = S;
     a.cps = cps;
     a.part = pb.ptr;
@@ -1486,7 +2056,11 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         /* double-buffered rows pay when a workgroup walks three or more chunks
          * (prefill, batched decode of many sequences); with one or two (the
          * 12-layer step) the extra LDS traffic does not */
-        if (fast && cps >= 3u)
+        if (pl.slab && pl.hg == 1u)
+            qsa_slab_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (pl.slab)
+            qsa_slab_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (fast && cps >= db_min_chunks())
             qsa_q8d256_k<MODE, true><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (fast)
             qsa_q8d256_k<MODE, false><<<grid, 256, 0, q4kv_stream>>>(a);
@@ -1500,7 +2074,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         if (S > 1u && !op) qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
     }
     if (op) {
-        if (!fast) return false;
+        if (!fast && !pl.slab) return false;
         a.item0 = 0;
         const uint32_t n_rb = (op->n_embd + OUT_RPB - 1u) / OUT_RPB;
         qsa_comb_gemv_k<MODE><<<dim3(a.n_head * n_rb, n_items / a.n_kvh), 256, 0, q4kv_stream>>>(
@@ -1622,7 +2196,7 @@ static bool step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32_t n
     a.seqs = (const q4kv_seq_desc *)d_descs;
     a.desc_stride = sizeof(q4kv_step_desc);
     const uint32_t gqa = n_head / n_kvh;
-    if (kv_f16 == Q4KV_Q8 && hd == 256u && gqa <= 8u)
+    if (step_fusable(kv_f16, hd, gqa))
         return launch_kind<Q4KV_Q8, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, nullptr, pb);
     /* other widths and shapes: the append launch, then the attention */
     const uint32_t row = kv_f16 == Q4KV_Q8 ? hd / 32u * 34u : hd * (kv_f16 == Q4KV_F16 ? 2u : 4u);
@@ -1687,10 +2261,16 @@ extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uin
     /* the same split division as q4_hip_qsa_step_batch (so the same results),
      * which must fit the static scratch */
     const uint32_t gqa = n_head / n_kvh, n_items = n_seq * n_kvh;
-    const uint32_t cp = kv_f16 == Q4KV_F32 ? KCfg<Q4KV_F32>::CP : KCfg<Q4KV_Q8>::CP;
-    uint32_t S, cps;
-    choose_split(n_items, (max_n + cp - 1u) / cp, gqa, q4kv_part != nullptr, q4kv_part_cap, S,
-                 cps);
+    const bool have = q4kv_part != nullptr;
+    const Plan pl =
+        step_fusable(kv_f16, hd, gqa)
+            ? plan_launch<Q4KV_Q8, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
+        : kv_f16 == Q4KV_F32
+            ? plan_launch<Q4KV_F32, MODE_BATCH>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
+        : kv_f16 == Q4KV_F16
+            ? plan_launch<Q4KV_F16, MODE_BATCH>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
+            : plan_launch<Q4KV_Q8, MODE_BATCH>(hd, n_items, max_n, gqa, have, q4kv_part_cap);
+    const uint32_t S = pl.S;
     const size_t need = S > 1u ? (size_t)n_items * S * gqa * PSTRIDE : 0u;
     if (need > Q4KV_SCRATCH_FLOATS) {
         Q4KV_ERR("qsa_step_batch_noalloc: %u items x %u splits need %zu floats of scratch, "
@@ -1719,8 +2299,8 @@ extern "C" bool q4_hip_qsa_step_prep_batch(const q4kv_prep_step_desc *d_descs, u
     if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
         return false;
     const uint32_t gqa = n_head / n_kvh;
-    if (kv_f16 != Q4KV_Q8 || hd != 256u || gqa > 8u || n_rot > hd) {
-        Q4KV_ERR("qsa_step_prep_batch: needs a q8_0 cache, hd 256, gqa <= 8, n_rot <= hd");
+    if (kv_f16 != Q4KV_Q8 || hd != 256u || !step_fusable(kv_f16, hd, gqa) || n_rot > hd) {
+        Q4KV_ERR("qsa_step_prep_batch: needs a q8_0 cache, hd 256, gqa <= 16, n_rot <= hd");
         return false;
     }
     (void)hipGetLastError();
@@ -1743,8 +2323,8 @@ extern "C" bool q4_hip_qsa_step_out_batch(const q4kv_step_desc *d_descs,
         !shape_ok(n_head, n_kvh, hd, kv_f16))
         return false;
     const uint32_t gqa = n_head / n_kvh;
-    if (kv_f16 != Q4KV_Q8 || hd != 256u || gqa > 8u || n_seq > 65535u) {
-        Q4KV_ERR("qsa_step_out_batch: needs a q8_0 cache, hd 256, gqa <= 8");
+    if (kv_f16 != Q4KV_Q8 || hd != 256u || !step_fusable(kv_f16, hd, gqa) || n_seq > 65535u) {
+        Q4KV_ERR("qsa_step_out_batch: needs a q8_0 cache, hd 256, gqa <= 16");
         return false;
     }
     (void)hipGetLastError();

@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 N_HEAD, N_KVH, HD = 16, 2, 256
 
 
-def _case(rng, oracle, n_seq, ctx, kind, pos_of, sel_of):
+def _case(rng, oracle, n_seq, ctx, kind, pos_of, sel_of, n_head=N_HEAD):
     """Host data of n_seq items: caches holding positions < pos, the new
     token's rows, queries and per-KV-head lists."""
     bpt = q4kv.token_bytes(kind, N_KVH, HD)
@@ -27,7 +27,7 @@ def _case(rng, oracle, n_seq, ctx, kind, pos_of, sel_of):
         k[pos:] = 0.0
         v[pos:] = 0.0
         kn, vn = heads(rng, (N_KVH,)), heads(rng, (N_KVH,))
-        q = heads(rng, (1, N_HEAD))
+        q = heads(rng, (1, n_head))
         sel = sel_of(rng, s, pos)
         enc = (lambda x: oracle.encode(x, kind))
         items.append(dict(pos=pos, kc=enc(k), vc=enc(v), kn=kn, vn=vn, q=q, sel=sel,
@@ -57,10 +57,11 @@ def _run(rt, items, ctx, kind, fused, dense=False):
         ptrs.append((kc, vc, do))
     max_n = max((it["pos"] + 1) if dense else it["sel"].shape[-1] for it in items)
     lib = rt.lib
+    nh = items[0]["q"].shape[1]
     if fused:
         dd = rt.alloc(ctypes.sizeof(steps))
         assert lib.q4_hip_h2d(dd, ctypes.addressof(steps), ctypes.sizeof(steps))
-        assert lib.q4_hip_qsa_step_batch(dd, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, kind, max_n)
+        assert lib.q4_hip_qsa_step_batch(dd, n_seq, nh, N_KVH, HD, 1.0 / 16, kind, max_n)
     else:
         da = rt.alloc(ctypes.sizeof(apps))
         ds = rt.alloc(ctypes.sizeof(seqs))
@@ -68,7 +69,7 @@ def _run(rt, items, ctx, kind, fused, dense=False):
         assert lib.q4_hip_h2d(ds, ctypes.addressof(seqs), ctypes.sizeof(seqs))
         bpt = q4kv.token_bytes(kind, N_KVH, HD)
         assert lib.q4_hip_kv_append_batch(da, n_seq, N_KVH * HD, bpt, kind)
-        assert lib.q4_hip_qsa_decode_batch(ds, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, kind, max_n)
+        assert lib.q4_hip_qsa_decode_batch(ds, n_seq, nh, N_KVH, HD, 1.0 / 16, kind, max_n)
     rt.sync()
     caches, outs = [], []
     for (kc, vc, do), it in zip(ptrs, items):
@@ -97,11 +98,11 @@ def _check(rt, oracle, items, ctx, kind, dense=False, what=""):
         k[p], v[p] = it["kn"], it["vn"]
         kq, vq = oracle.encode(k, kind), oracle.encode(v, kind)
         if dense:
-            want = oracle.attn(it["q"], kq, vq, kind, N_HEAD, N_KVH, HD, 1, kv_base=p,
+            want = oracle.attn(it["q"], kq, vq, kind, it["q"].shape[1], N_KVH, HD, 1, kv_base=p,
                                max_kv=ctx, scale=1.0 / 16)
         else:
             w = it["sel"].shape[-1]
-            want = oracle.attn(it["q"], kq, vq, kind, N_HEAD, N_KVH, HD, 1, idx=it["sel"],
+            want = oracle.attn(it["q"], kq, vq, kind, it["q"].shape[1], N_KVH, HD, 1, idx=it["sel"],
                                width=w, tok_stride=N_KVH * w, kvh_stride=w, max_kv=ctx,
                                scale=1.0 / 16)
         assert_attn_close(o1[s], want, what=f"{what} item {s}")
@@ -158,3 +159,34 @@ def test_step_batch_other_widths(rt, oracle, kind):
     ctx = 4096
     items, _ = _case(rng, oracle, 3, ctx, kind, lambda s: ctx - 1 - 300 * s, _sel_kv)
     _check(rt, oracle, items, ctx, kind, what=f"width {kind}")
+
+
+@pytest.mark.parametrize("n_head", [24, 32, 18])
+def test_step_batch_q8_more_heads_per_kv_head(rt, oracle, n_head):
+    """The production layout (24 query heads over 2 KV heads, 12 per KV head),
+    16 per KV head, and an odd 9: the fused step of two head groups against
+    append + batched decode, and against the oracle."""
+    rng = np.random.default_rng(950 + n_head)
+    ctx = 16384
+    items, _ = _case(rng, oracle, 12, ctx, q4kv.KV_Q8, lambda s: ctx - 1 - 300 * s, _sel_kv,
+                     n_head=n_head)
+    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what=f"q8 12 layers, {n_head} heads")
+
+
+def test_step_batch_more_heads_position_anywhere(rt, oracle):
+    """24 heads: the new position first, in a middle split, twice, or not at all."""
+    rng = np.random.default_rng(960)
+    ctx = 8192
+
+    def sel_of(rng, s, pos):
+        base = np.stack([selection(rng, pos - 1) for _ in range(N_KVH)])
+        if s == 0:
+            base[:, 0] = pos
+        elif s == 1:
+            base[:, 1000] = pos
+        elif s == 2:
+            base[:, 70] = pos
+            base[:, 2000] = pos
+        return base
+    items, _ = _case(rng, oracle, 4, ctx, q4kv.KV_Q8, lambda s: 5000 + 37 * s, sel_of, n_head=24)
+    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what="24 heads, position anywhere")

@@ -18,7 +18,7 @@ N_HEAD, N_KVH, HD = 16, 2, 256
 N_ROT, BASE, EPS = 64, 1.0e7, 1.0e-6
 
 
-def _items(rng, oracle, n_seq, ctx, width):
+def _items(rng, oracle, n_seq, ctx, width, n_head=N_HEAD):
     items = []
     for s in range(n_seq):
         pos = ctx - 1 - 97 * s
@@ -30,8 +30,8 @@ def _items(rng, oracle, n_seq, ctx, width):
                             for _ in range(N_KVH)])
         else:
             sel = np.stack([selection(rng, pos) for _ in range(N_KVH)])
-        q = heads(rng, (N_HEAD,))
-        gate = rng.standard_normal((N_HEAD, HD)).astype(np.float32)
+        q = heads(rng, (n_head,))
+        gate = rng.standard_normal((n_head, HD)).astype(np.float32)
         items.append(dict(pos=pos, kc=oracle.encode(k, q4kv.KV_Q8),
                           vc=oracle.encode(v, q4kv.KV_Q8), k=k, v=v,
                           kn=heads(rng, (N_KVH,)) * 3, vn=heads(rng, (N_KVH,)),
@@ -46,6 +46,7 @@ def _run(rt, items, ctx, fused):
     lib = rt.lib
     before = set(rt._owned)
     n = len(items)
+    nh = items[0]["qg"].shape[0]
     steps = (q4kv.StepDesc * n)()
     preps = (q4kv.PrepStepDesc * n)()
     keep = []
@@ -53,17 +54,17 @@ def _run(rt, items, ctx, fused):
         kc, vc = rt.upload(it["kc"]), rt.upload(it["vc"])
         dqg, dkn, dvn = rt.upload(it["qg"]), rt.upload(it["kn"]), rt.upload(it["vn"])
         dwq, dwk = rt.upload(it["wq"]), rt.upload(it["wk"])
-        dg = rt.upload(np.full((N_HEAD, HD), np.nan, np.float32))
-        do = rt.upload(np.full((N_HEAD, HD), np.nan, np.float32))
+        dg = rt.upload(np.full((nh, HD), np.nan, np.float32))
+        do = rt.upload(np.full((nh, HD), np.nan, np.float32))
         di = rt.upload(it["sel"])
         w = it["sel"].shape[-1]
         if fused:
             seq = q4kv.SeqDesc(kc, vc, dqg, dg, do, di, w, w, ctx, 0)
             preps[s] = q4kv.PrepStepDesc(q4kv.StepDesc(seq, dkn, dvn, it["pos"]), dwq, dwk)
         else:
-            dq = rt.alloc(N_HEAD * HD * 4)
+            dq = rt.alloc(nh * HD * 4)
             dk = rt.upload(it["kn"])                       # k_prep works in place
-            assert lib.q4_hip_qsa_q_prep(dqg, dwq, dq, dg, N_HEAD, HD, N_ROT, it["pos"], BASE, EPS)
+            assert lib.q4_hip_qsa_q_prep(dqg, dwq, dq, dg, nh, HD, N_ROT, it["pos"], BASE, EPS)
             assert lib.q4_hip_qsa_k_prep(dk, dwk, N_KVH, HD, N_ROT, it["pos"], BASE, EPS)
             seq = q4kv.SeqDesc(kc, vc, dq, dg, do, di, w, w, ctx, 0)
             steps[s] = q4kv.StepDesc(seq, dk, dvn, it["pos"])
@@ -73,17 +74,17 @@ def _run(rt, items, ctx, fused):
     dd = rt.alloc(ctypes.sizeof(arr))
     assert lib.q4_hip_h2d(dd, ctypes.addressof(arr), ctypes.sizeof(arr))
     if fused:
-        assert lib.q4_hip_qsa_step_prep_batch(dd, n, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8,
+        assert lib.q4_hip_qsa_step_prep_batch(dd, n, nh, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8,
                                               max_n, N_ROT, BASE, EPS)
     else:
-        assert lib.q4_hip_qsa_step_batch(dd, n, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, max_n)
+        assert lib.q4_hip_qsa_step_batch(dd, n, nh, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, max_n)
     rt.sync()
     res = []
     for (kc, vc, dg, do, dkn), it in zip(keep, items):
         res.append(dict(kc=rt.download(kc, it["kc"].nbytes, np.uint8),
                         vc=rt.download(vc, it["vc"].nbytes, np.uint8),
-                        g=rt.download(dg, N_HEAD * HD * 4, np.float32),
-                        out=rt.download(do, N_HEAD * HD * 4, np.float32).reshape(1, N_HEAD, HD),
+                        g=rt.download(dg, nh * HD * 4, np.float32),
+                        out=rt.download(do, nh * HD * 4, np.float32).reshape(1, nh, HD),
                         kn=rt.download(dkn, it["kn"].nbytes, np.float32)))
     for p in [p for p in rt._owned if p not in before]:
         rt.free(p)
@@ -91,20 +92,24 @@ def _run(rt, items, ctx, fused):
 
 
 # 32 sequences: five chunks per workgroup, the double-buffered instance
-@pytest.mark.parametrize("n_seq,ctx,width", [(12, 16384, 0), (3, 4096, 40), (32, 16384, 0)])
-def test_step_prep_matches_prep_then_step(rt, oracle, n_seq, ctx, width):
+# 24 heads over 2 KV heads (12 per KV head): the production layout, two head
+# groups per workgroup
+@pytest.mark.parametrize("n_seq,ctx,width,n_head", [(12, 16384, 0, 16), (3, 4096, 40, 16),
+                                                     (32, 16384, 0, 16), (12, 16384, 0, 24),
+                                                     (3, 4096, 40, 24)])
+def test_step_prep_matches_prep_then_step(rt, oracle, n_seq, ctx, width, n_head):
     """12 layers of 2051-entry lists (split-KV with a merge), and 40-entry
     lists (one split: the kernel's own epilogue applies the gate)."""
-    note(f"step_prep n_seq={n_seq} width={width}")
-    rng = np.random.default_rng(910 + n_seq)
-    items = _items(rng, oracle, n_seq, ctx, width)
+    note(f"step_prep n_seq={n_seq} width={width} n_head={n_head}")
+    rng = np.random.default_rng(910 + n_seq + n_head)
+    items = _items(rng, oracle, n_seq, ctx, width, n_head)
     a = _run(rt, items, ctx, fused=True)
     b = _run(rt, items, ctx, fused=False)
     for s, it in enumerate(items):
         for key in ("kc", "vc", "g", "out"):
             assert np.array_equal(a[s][key].view(np.uint8), b[s][key].view(np.uint8)), (s, key)
         assert np.array_equal(a[s]["kn"], it["kn"].ravel())     # raw K not modified
-        assert np.array_equal(a[s]["g"].reshape(N_HEAD, HD), it["qg"][:, HD:])
+        assert np.array_equal(a[s]["g"].reshape(n_head, HD), it["qg"][:, HD:])
         # against the oracle: attention of the prepared query over the cache
         # holding the prepared, quantised key
         p = it["pos"]
@@ -114,7 +119,7 @@ def test_step_prep_matches_prep_then_step(rt, oracle, n_seq, ctx, width):
         k[p], v[p] = kp, it["vn"]
         kq, vq = oracle.encode(k, q4kv.KV_Q8), oracle.encode(v, q4kv.KV_Q8)
         w = it["sel"].shape[-1]
-        want = oracle.attn(qp, kq, vq, q4kv.KV_Q8, N_HEAD, N_KVH, HD, 1,
+        want = oracle.attn(qp, kq, vq, q4kv.KV_Q8, n_head, N_KVH, HD, 1,
                            gate=it["qg"][None, :, HD:], idx=it["sel"], width=w,
                            tok_stride=N_KVH * w, kvh_stride=w, max_kv=ctx, scale=1.0 / 16)
         assert_attn_close(a[s]["out"], want, what=f"step_prep item {s}")
