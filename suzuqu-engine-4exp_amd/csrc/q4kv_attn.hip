@@ -1987,12 +1987,15 @@ struct Plan {
     uint32_t S, cps;
 };
 
-/* The slab kernel takes q8_0 / hd 256 decode shapes with 9 to 16 query heads
- * per KV head (two head groups; up to 8 heads the chunk kernel qsa_q8d256_k
- * measures faster), while the launch stays small enough that its splits of
- * 64 list entries keep the chip busy without a flood of partials;
- * prefill-sized launches keep the chunk-streaming kernel. Q4KV_SLAB=0 turns
- * it off, Q4KV_SLAB=2 uses it from one head up (A/B measurement). */
+/* The slab kernel takes q8_0 / hd 256 shapes with 9 to 16 query heads per KV
+ * head (two head groups), and prefill-sized launches of any head count, whose
+ * workgroups then stream their passes (each wave's online softmax carried
+ * across them): there its lower VALU work per position wins (config 3: 2.82
+ * vs 3.67 ms per layer). Decode launches with up to 8 query heads per KV head
+ * keep the chunk kernel qsa_q8d256_k, whose shorter per-workgroup chain
+ * measures faster there (18.7 vs 19.9 us for the 12-layer step).
+ * Q4KV_SLAB=0 turns the slab kernel off, Q4KV_SLAB=2 uses it everywhere
+ * (A/B measurement). */
 #define SLAB_MAX_WG 16384u
 static int slab_mode(void) {
     static int v = -1;
@@ -2002,20 +2005,23 @@ static int slab_mode(void) {
     }
     return v;
 }
-static bool slab_takes(uint32_t gqa) {
+static bool slab_takes(uint32_t gqa, bool prefill_sized) {
     const int m = slab_mode();
-    return gqa <= 16u && (m == 2 || (m == 1 && gqa > 8u));
+    return gqa <= 16u && (m == 2 || (m == 1 && (gqa > 8u || prefill_sized)));
 }
 
 template <int KIND, int MODE>
 static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t gqa,
                         bool have_part, size_t cap) {
     Plan pl = {false, 1u, 1u, 1u};
-    if (KIND == Q4KV_Q8 && hd == 256u && slab_takes(gqa)) {
-        const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
-        uint32_t S = (max_n + ne - 1u) / ne;
+    const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
+    const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
+    const bool prefill_sized = (uint64_t)n_items * s_full > SLAB_MAX_WG;
+    if (KIND == Q4KV_Q8 && hd == 256u && slab_takes(gqa, prefill_sized)) {
+        /* many items (prefill): fewer splits, each wave streaming its passes */
+        uint32_t S = !prefill_sized ? s_full : n_items >= SLAB_MAX_WG ? 1u : SLAB_MAX_WG / n_items;
         if (S < 1u) S = 1u;
-        if ((uint64_t)n_items * S <= SLAB_MAX_WG) {
+        {
             if (S > COMB_MAXS) S = COMB_MAXS;
             const size_t per = (size_t)gqa * PSTRIDE;
             while (S > 1u && (size_t)n_items * S * per > cap) S--; /* waves then loop */
@@ -2034,7 +2040,7 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
 
 /* A fused append + attention launch exists for this shape. */
 static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
-    return kind == Q4KV_Q8 && hd == 256u && (gqa <= 8u || slab_takes(gqa));
+    return kind == Q4KV_Q8 && hd == 256u && (gqa <= 8u || slab_takes(gqa, false));
 }
 
 template <int KIND, int MODE>
