@@ -69,6 +69,11 @@ struct AttnArgs {
     /* MODE_PSTEP */
     uint32_t n_rot;
     float rope_base, eps;
+    /* prefill band (MODE_INDEXED): per item, the list entries before its
+     * band (the slab kernel's list length) and the band's (m, l) per head;
+     * the band's unnormalised output rows are in out */
+    int32_t *band_nb;
+    float *band_ml;
 };
 
 struct Item {
@@ -1341,7 +1346,10 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     const uint32_t k_esel = jg == 3u ? 0x05040302u : 0x07060504u;
     uint8_t *const krow = rows + slab * SLAB * ROWB;
     uint8_t *const vrow = rows + NE * ROWB + slab * SLAB * ROWB;
-    const uint32_t n = it.n;
+    /* with a prefill band, the list entries from the band on are the band
+     * kernel's */
+    const bool band = MODE == MODE_INDEXED && a.band_nb != nullptr;
+    const uint32_t n = band ? min((uint32_t)ldg(a.band_nb + item), it.n) : it.n;
     const uint32_t j0 = (uint32_t)(((uint64_t)s * n) / a.S);
     const uint32_t j1 = (uint32_t)(((uint64_t)(s + 1u) * n) / a.S);
     /* passes: every wave of the workgroup runs the same number (barriers
@@ -1600,6 +1608,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             mx = max32(max16(mx));
             const float mn = fmax2(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+            const bool grew = mn > m_run;
             m_run = mn;
             float P[8], ls = 0.f;
 #pragma unroll
@@ -1608,7 +1617,9 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
                 ls += P[i];
             }
             l_run = l_run * alpha + ls;
-            if (pass > 0u) {
+            /* later passes: rescale only when some column's maximum grew
+             * (alpha is 1 elsewhere) */
+            if (pass > 0u && __ballot(grew) != 0u) {
 #pragma unroll
                 for (uint32_t t = 0; t < 16u; t++) acc[t] *= alpha;
             }
@@ -1632,14 +1643,16 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
                                  split_pk(u[4], u[5], nsel), split_pk(u[6], u[7], nsel)};
                 const h8_t B = __builtin_bit_cast(h8_t, bw);
                 /* V^T: dims 2c, 2c + 1 of block b at the lane's 8 positions */
+                /* each 16-bit read holds dims 2c, 2c + 1 of one position; two
+                 * positions' even (odd) bytes go to one fp16 pair, which the
+                 * xor turns into 1024 + (b ^ 0x80) = 1152 + b */
                 u4_t E, O;
 #pragma unroll
                 for (uint32_t k = 0; k < 4u; k++) {
                     const uint8_t *vd = (k < 2u ? s0 : s1) + 2u + 2u * c + (2u * (k & 1u)) * ROWB;
-                    uint32_t x = lds_u16x2(vd, vd + ROWB);
-                    x ^= 0x80808080u;
-                    E[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04020400u);
-                    O[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04030401u);
+                    const uint32_t x0 = *(const uint16_t *)vd, x1 = *(const uint16_t *)(vd + ROWB);
+                    E[k] = __builtin_amdgcn_perm(x1, x0, 0x0C040C00u) ^ 0x64806480u;
+                    O[k] = __builtin_amdgcn_perm(x1, x0, 0x0C050C01u) ^ 0x64806480u;
                 }
                 acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     __builtin_bit_cast(h8_t, E), B, acc[2u * b], 0, 0, 0);
@@ -1678,9 +1691,18 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         const uint32_t thg = task >> 9, hh = (task >> 6) & 7u, t = (task >> 2) & 15u, jq = task & 3u;
         const uint32_t g = 8u * thg + hh;
         if (g >= gqa) continue;
+        const uint32_t col = 16u * t + 4u * jq;
         float Mh = -INFINITY;
 #pragma unroll
         for (uint32_t w = thg; w < 4u; w += HG) Mh = fmax2(Mh, s_m[w][hh]);
+        /* the band's partial of this (item, head), if any (single split) */
+        float mb = -INFINITY, lb = 0.f;
+        if (band && a.S == 1u) {
+            const fv2 ml = ldg((const fv2 *)(a.band_ml + ((size_t)item * gqa + g) * 2u));
+            mb = ml[0];
+            lb = ml[1];
+            if (lb > 0.f) Mh = fmax2(Mh, mb);
+        }
         float L = 0.f;
         f4_t v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1690,7 +1712,13 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             L += fw * s_l[w][hh];
             v += fw * *(const f4_t *)(mrg + ((w * 16u + t) * 8u + hh) * 20u + 4u * jq);
         }
-        const uint32_t col = 16u * t + 4u * jq;
+        if (lb > 0.f) {
+            const float fb = __builtin_amdgcn_exp2f(mb - Mh);
+            L += fb * lb;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++)
+                v[i] += fb * ldg(it.out + (size_t)g * 256u + col_dim<Q4KV_Q8>(col + i));
+        }
         if (a.S == 1u) {
             const float inv = L > 0.f ? 1.f / L : 0.f;
 #pragma unroll
@@ -1714,6 +1742,381 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         }
     }
     TRACEW(10);
+}
+
+/* ------------------------------------------------------------------------
+ * Prefill band kernel: the recent window that consecutive prefill tokens'
+ * lists share, as dense MFMA tiles. A token's band is the longest run of
+ * consecutive positions that ends its list (the causal recent window); the
+ * slab kernel then attends only the list entries before it. One workgroup
+ * takes BAND_TOK consecutive tokens of one KV head (two per wave): the union
+ * of their bands (at most BAND_SPAN positions) streams through LDS 32
+ * positions per pass (two passes in flight), where the workgroup dequantises
+ * the K and V rows once into fp16 hi + lo parts (k * scale, exact to
+ * ~2^-22), shared by every token and head of the tile. Each wave then runs,
+ * for its two tokens with every LDS operand read once for both,
+ *   S^T = K' Q^T   (A = K' hi / lo rows, B = a token's Q^T, columns 0-7 the
+ *                   fp16 part of 8 heads' q, 8-15 the residual),
+ *   softmax over the token's band positions only (the rest -inf),
+ *   O^T += V'^T P^T (A = V'^T hi / lo, B = the weights split hi / lo),
+ * with no per-position scale work on the VALU. The result is the (m, l,
+ * unnormalised acc) partial of each (token, head), handed to the slab
+ * kernel's final merge.
+ * ------------------------------------------------------------------------ */
+constexpr uint32_t BAND_TPW = 2;                /* tokens per wave */
+constexpr uint32_t BAND_WAVES = 8;              /* waves per workgroup */
+constexpr uint32_t BAND_TOK = BAND_WAVES * BAND_TPW; /* tokens per workgroup */
+constexpr uint32_t BAND_MIN = 64;               /* shortest run worth a band */
+constexpr uint32_t BAND_SPAN = 1024;            /* widest union of a workgroup's bands */
+constexpr uint32_t BP = 32;                     /* positions per pass */
+
+/* 16 bytes global -> LDS like dma16, issued from inline assembly so that the
+ * compiler does not add its own wait for the DMA before every LDS read of
+ * the staging buffers (it cannot tell the two buffers apart); the band
+ * kernel waits for its DMAs itself, with explicit vmcnt counts. */
+__device__ static inline void dma16_manual(const void *src, void *lds_wave_base) {
+    const uint32_t m0 =
+        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(LOCAL void *)lds_wave_base);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0), "v"((const GLOBAL void *)src)
+                 : "memory", "m0");
+}
+/* workgroup barrier that waits for this wave's LDS accesses only (the
+ * __syncthreads fence also drains every outstanding global load, including
+ * the next pass's DMA) */
+__device__ static inline void barrier_lds(void) {
+    __builtin_amdgcn_s_waitcnt(0xC07F); /* lgkmcnt(0) */
+    __builtin_amdgcn_s_barrier();
+}
+
+/* The band of one token's list (wave-uniform): the run of consecutive
+ * positions that ends it (after any padding), at least BAND_MIN long.
+ * Returns the list index where the run starts (width if there is none) and
+ * the run's first and last positions (ps > pe if none). */
+__device__ static inline uint32_t band_of(const int32_t *list, uint32_t width, uint32_t max_kv,
+                                          uint32_t lane, int32_t &ps, int32_t &pe) {
+    ps = 1;
+    pe = 0;
+    int32_t e = -1, vend = 0;
+    for (int32_t base = (int32_t)width - 64;; base -= 64) {
+        const int32_t j = base + (int32_t)lane;
+        const int32_t v = j >= 0 ? ldg(list + j) : -1;
+        const bool ok = j >= 0 && v >= 0 && (uint32_t)v < max_kv;
+        const uint64_t bal = __ballot(ok);
+        if (bal) {
+            const uint32_t hi = 63u - (uint32_t)__builtin_clzll(bal);
+            e = base + (int32_t)hi;
+            vend = __shfl(v, (int)hi);
+            break;
+        }
+        if (base <= 0) break;
+    }
+    if (e < 0) return width;
+    uint32_t run = 0;
+    for (uint32_t w0 = 0; w0 < BAND_SPAN; w0 += 64u) {
+        const int32_t j = e - (int32_t)(w0 + lane);
+        const bool ok = j >= 0 && ldg(list + j) == vend - (int32_t)(w0 + lane);
+        const uint64_t bad = __ballot(!ok);
+        if (bad) {
+            run = w0 + (uint32_t)__builtin_ctzll(bad);
+            break;
+        }
+        run = w0 + 64u;
+    }
+    if (run > BAND_SPAN) run = BAND_SPAN;
+    if (run < BAND_MIN) return width;
+    ps = vend - (int32_t)run + 1;
+    pe = vend;
+    return (uint32_t)(e - (int32_t)run + 1);
+}
+
+__global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
+    constexpr uint32_t ROWB = 272, NCH = 17, KPAD = 264, VPAD = 40, TW = BAND_TPW;
+    /* K rows | V rows of even and odd passes: two passes in flight (two
+     * objects, so the LDS-DMA wait before reading one buffer does not cover
+     * the other's DMA) */
+    __shared__ __attribute__((aligned(16))) uint8_t rawA[2 * BP * ROWB];
+    __shared__ __attribute__((aligned(16))) uint8_t rawB[2 * BP * ROWB];
+    /* K' [hi/lo][position][dim] and V'^T [hi/lo][dim][slot] (fp16); V slot
+     * 8 g + i holds position 4 g + i (i < 4) or 16 + 4 g + i - 4, the
+     * positions a lane of k-group g holds in the score tiles */
+    __shared__ __attribute__((aligned(16))) _Float16 kp[2][BP][KPAD];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][256][VPAD];
+    __shared__ int32_t s_ps[BAND_TOK], s_pe[BAND_TOK];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t kh = blockIdx.y, t0 = blockIdx.x * BAND_TOK + wave * TW;
+    const uint32_t n_tok = a.kv_base; /* tokens of the launch (set by the host) */
+    const uint32_t gqa = a.n_head / a.n_kvh, width = a.width;
+    const uint32_t c = lane & 15u, jg = lane >> 4;
+    const float nsel = c >= 8u ? -1.f : 0.f;
+    const size_t rstride = (size_t)a.n_kvh * ROWB;
+    const uint8_t *kbase = a.kc + (size_t)kh * ROWB, *vbase = a.vc + (size_t)kh * ROWB;
+
+    TRACEW(0);
+    /* ---- the bands of this wave's tokens ---- */
+    int32_t ps[TW], pe[TW];
+    uint32_t nb[TW];
+#pragma unroll
+    for (uint32_t k = 0; k < TW; k++) {
+        const uint32_t t = t0 + k;
+        ps[k] = 1;
+        pe[k] = 0;
+        nb[k] = width;
+        if (t < n_tok)
+            nb[k] = band_of(a.idx + (size_t)t * a.tok_stride + (size_t)kh * a.kvh_stride, width,
+                            a.max_kv, lane, ps[k], pe[k]);
+        if (lane == 0) {
+            s_ps[wave * TW + k] = ps[k];
+            s_pe[wave * TW + k] = pe[k];
+        }
+    }
+    __syncthreads();
+    int32_t lo = INT32_MAX, hi = INT32_MIN;
+#pragma unroll
+    for (uint32_t w = 0; w < BAND_TOK; w++)
+        if (s_ps[w] <= s_pe[w]) {
+            lo = min(lo, s_ps[w]);
+            hi = max(hi, s_pe[w]);
+        }
+    const bool tile = lo <= hi && (int64_t)hi - lo + 1 <= (int64_t)BAND_SPAN;
+#pragma unroll
+    for (uint32_t k = 0; k < TW; k++) {
+        const uint32_t t = t0 + k;
+        if (!tile) {
+            ps[k] = 1;
+            pe[k] = 0;
+            nb[k] = width;
+        }
+        if (t < n_tok) {
+            const uint32_t item = t * a.n_kvh + kh;
+            if (lane == 0) a.band_nb[item] = (int32_t)nb[k];
+            if (ps[k] > pe[k] && lane < gqa)
+                stg((fv2 *)(a.band_ml + ((size_t)item * gqa + lane) * 2u), (fv2){-INFINITY, 0.f});
+        }
+    }
+    if (!tile) return; /* uniform over the workgroup */
+    TRACEW(1);
+    const uint32_t n_pass = (uint32_t)(hi - lo) / BP + 1u;
+
+    /* the Q^T operands of this wave's tokens, natural dim order */
+    h8_t qB[TW][8];
+#pragma unroll
+    for (uint32_t k = 0; k < TW; k++) {
+        const uint32_t t = t0 + k, h = c & 7u;
+        const bool hv = t < n_tok && h < gqa;
+        const float qs = hv ? a.scale_log2 : 0.f;
+        const float *qr = a.q + ((size_t)(t < n_tok ? t : 0u) * a.n_head + kh * gqa + (hv ? h : 0u)) * 256u;
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++) {
+            const f4_t x0 = ldg((const f4_t *)(qr + 32u * b + 8u * jg));
+            const f4_t x1 = ldg((const f4_t *)(qr + 32u * b + 8u * jg + 4u));
+            qB[k][b] = __builtin_bit_cast(
+                h8_t, (u4_t){split_pk(x0[0] * qs, x0[1] * qs, nsel), split_pk(x0[2] * qs, x0[3] * qs, nsel),
+                             split_pk(x1[0] * qs, x1[1] * qs, nsel), split_pk(x1[2] * qs, x1[3] * qs, nsel)});
+        }
+    }
+
+    /* the rows of pass p: 32 positions x 17 sixteen-byte pieces per cache;
+     * wave w issues K and V instruction w (and wave 0 / 1 the ninth) */
+    auto issue = [&](uint32_t pass, uint8_t *rawb) {
+        const int32_t base = lo + (int32_t)(pass * BP);
+        /* K and V instruction u = wave; wave 0 / 1 also the ninth K / V
+         * instruction */
+#pragma unroll
+        for (uint32_t k = 0; k < 2u; k++) {
+            const uint32_t u = k == 0u ? wave : 8u;
+            if (k == 1u && wave > 1u) break;
+            const uint32_t e = u * 64u + lane;
+            const uint32_t r = e / NCH, q = e - r * NCH;
+            int32_t p = base + (int32_t)r;
+            if (p > hi || (uint32_t)p >= a.max_kv) p = lo; /* outside every band: masked */
+            const size_t off = (size_t)p * rstride + q * 16u;
+            if (u < 8u || lane < 32u) {
+                if (k == 0u || wave == 0u) dma16_manual(kbase + off, rawb + u * 1024u);
+                if (k == 0u || wave == 1u) dma16_manual(vbase + off, rawb + BP * ROWB + u * 1024u);
+            }
+        }
+    };
+    /* the Q operands are complete before the first DMA: a compiler wait for
+     * a load issued after the (assembly) DMAs would drain those too */
+#pragma unroll
+    for (uint32_t k = 0; k < TW; k++)
+#pragma unroll
+        for (uint32_t bb = 0; bb < 8u; bb++) asm volatile("" ::"v"(qB[k][bb]));
+    TRACEW(2);
+    issue(0u, rawA);
+    if (n_pass > 1u) issue(1u, rawB);
+
+    float m_run[TW], l_run[TW];
+    f4_t acc[TW][16];
+#pragma unroll
+    for (uint32_t k = 0; k < TW; k++) {
+        m_run[k] = -INFINITY;
+        l_run[k] = 0.f;
+#pragma unroll
+        for (uint32_t T = 0; T < 16u; T++) acc[k][T] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    }
+
+    auto run_pass = [&](uint32_t pass, uint8_t *rawb) {
+        /* this pass's rows landed (the next pass's may still be in flight:
+         * s_waitcnt vmcnt(n) with the lgkm / exp counts unconstrained; waves
+         * 0 and 1 issue three DMA instructions per pass, the others two) */
+        if (pass + 1u < n_pass) {
+            if (wave <= 1u)
+                __builtin_amdgcn_s_waitcnt(0x0F73);
+            else
+                __builtin_amdgcn_s_waitcnt(0x0F72);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        barrier_lds(); /* rows landed; every wave done with the last pass */
+        if (pass == 4u) TRACEW(3);
+        /* ---- dequantise: K' rows (work item: position x >> 4, 16 dims) ---- */
+#pragma unroll
+        for (uint32_t x = tid; x < 512u; x += 64u * BAND_WAVES) {
+            const uint32_t p = x >> 4, d0 = 16u * (x & 15u), b = d0 >> 5;
+            const uint8_t *src = rawb + p * ROWB + 34u * b + 2u + (d0 & 31u);
+            const float ks = ld_h(rawb + p * ROWB + 34u * b);
+            uint32_t hw[8], lw[8];
+#pragma unroll
+            for (uint32_t i = 0; i < 8u; i++) {
+                const uint32_t w = *(const uint16_t *)(src + 2u * i);
+                const float x0 = (float)(int32_t)(int8_t)(w & 0xffu) * ks;
+                const float x1 = (float)(int32_t)(int8_t)(w >> 8) * ks;
+                hw[i] = pkrtz(x0, x1);
+                lw[i] = pkrtz(x0 - h2lo(hw[i]), x1 - h2hi(hw[i]));
+            }
+            *(u4_t *)&kp[0][p][d0] = (u4_t){hw[0], hw[1], hw[2], hw[3]};
+            *(u4_t *)&kp[0][p][d0 + 8u] = (u4_t){hw[4], hw[5], hw[6], hw[7]};
+            *(u4_t *)&kp[1][p][d0] = (u4_t){lw[0], lw[1], lw[2], lw[3]};
+            *(u4_t *)&kp[1][p][d0 + 8u] = (u4_t){lw[4], lw[5], lw[6], lw[7]};
+        }
+        /* ---- V'^T (work item: dims 2 dp, 2 dp + 1, slots 8 g .. 8 g + 7) ---- */
+#pragma unroll
+        for (uint32_t x = tid; x < 512u; x += 64u * BAND_WAVES) {
+            const uint32_t dp = x & 127u, g = x >> 7, b = dp >> 4;
+            const uint8_t *vr = rawb + BP * ROWB;
+            uint32_t he[4], le[4], ho[4], lo4[4];
+#pragma unroll
+            for (uint32_t i2 = 0; i2 < 4u; i2++) {
+                float xe[2], xo[2];
+#pragma unroll
+                for (uint32_t k = 0; k < 2u; k++) {
+                    const uint32_t i = 2u * i2 + k;
+                    const uint32_t p = i < 4u ? 4u * g + i : 16u + 4u * g + i - 4u;
+                    const uint8_t *row = vr + p * ROWB + 34u * b;
+                    const float vs = ld_h(row);
+                    const uint32_t w = *(const uint16_t *)(row + 2u + 2u * (dp & 15u));
+                    xe[k] = (float)(int32_t)(int8_t)(w & 0xffu) * vs;
+                    xo[k] = (float)(int32_t)(int8_t)(w >> 8) * vs;
+                }
+                he[i2] = pkrtz(xe[0], xe[1]);
+                le[i2] = pkrtz(xe[0] - h2lo(he[i2]), xe[1] - h2hi(he[i2]));
+                ho[i2] = pkrtz(xo[0], xo[1]);
+                lo4[i2] = pkrtz(xo[0] - h2lo(ho[i2]), xo[1] - h2hi(ho[i2]));
+            }
+            *(u4_t *)&vt[0][2u * dp][8u * g] = (u4_t){he[0], he[1], he[2], he[3]};
+            *(u4_t *)&vt[1][2u * dp][8u * g] = (u4_t){le[0], le[1], le[2], le[3]};
+            *(u4_t *)&vt[0][2u * dp + 1u][8u * g] = (u4_t){ho[0], ho[1], ho[2], ho[3]};
+            *(u4_t *)&vt[1][2u * dp + 1u][8u * g] = (u4_t){lo4[0], lo4[1], lo4[2], lo4[3]};
+        }
+        barrier_lds(); /* K', V'^T ready; this pass's raw rows are free */
+        if (pass == 4u) TRACEW(4);
+        if (pass + 2u < n_pass) issue(pass + 2u, rawb);
+        const int32_t base = lo + (int32_t)(pass * BP);
+        bool live[TW], any = false;
+#pragma unroll
+        for (uint32_t k = 0; k < TW; k++) {
+            live[k] = ps[k] <= pe[k] && base <= pe[k] && base + (int32_t)BP - 1 >= ps[k];
+            any = any || live[k];
+        }
+        if (!any) return; /* wave-uniform */
+        if (pass == 4u) TRACEW(5);
+        /* ---- scores of the tokens' 8 heads at the pass's 32 positions ---- */
+        f4_t S[TW][2];
+#pragma unroll
+        for (uint32_t k = 0; k < TW; k++) S[k][0] = S[k][1] = (f4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++) {
+#pragma unroll
+            for (uint32_t tt = 0; tt < 2u; tt++) {
+#pragma unroll
+                for (uint32_t hl = 0; hl < 2u; hl++) {
+                    const h8_t A = *(const h8_t *)&kp[hl][16u * tt + c][32u * b + 8u * jg];
+#pragma unroll
+                    for (uint32_t k = 0; k < TW; k++)
+                        S[k][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, qB[k][b], S[k][tt], 0, 0, 0);
+                }
+            }
+        }
+        h8_t B[TW];
+#pragma unroll
+        for (uint32_t k = 0; k < TW; k++) {
+            float T[8];
+#pragma unroll
+            for (uint32_t i = 0; i < 8u; i++) {
+                const int32_t P = base + (int32_t)((i < 4u ? 0u : 16u) + 4u * jg + (i & 3u));
+                const float x = add_ror8(S[k][i >> 2][i & 3u]);
+                T[i] = (P >= ps[k] && P <= pe[k]) ? x : -INFINITY;
+            }
+            float mx = fmax3v(fmax3v(T[0], T[1], T[2]), fmax3v(T[3], T[4], T[5]), fmax2(T[6], T[7]));
+            mx = max32(max16(mx));
+            const float mn = fmax2(m_run[k], mx);
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            const float alpha = __builtin_amdgcn_exp2f(m_run[k] - ms);
+            const bool grew = mn > m_run[k];
+            m_run[k] = mn;
+            float P[8], ls = 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < 8u; i++) {
+                P[i] = __builtin_amdgcn_exp2f(T[i] - ms);
+                ls += P[i];
+            }
+            l_run[k] = l_run[k] * alpha + ls;
+            if (__ballot(grew) != 0u) {
+#pragma unroll
+                for (uint32_t T2 = 0; T2 < 16u; T2++) acc[k][T2] *= alpha;
+            }
+            B[k] = __builtin_bit_cast(
+                h8_t, (u4_t){split_pk(P[0], P[1], nsel), split_pk(P[2], P[3], nsel),
+                             split_pk(P[4], P[5], nsel), split_pk(P[6], P[7], nsel)});
+        }
+#pragma unroll
+        for (uint32_t T2 = 0; T2 < 16u; T2++) {
+#pragma unroll
+            for (uint32_t hl = 0; hl < 2u; hl++) {
+                const h8_t A = *(const h8_t *)&vt[hl][16u * T2 + c][8u * jg];
+#pragma unroll
+                for (uint32_t k = 0; k < TW; k++)
+                    acc[k][T2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[k], acc[k][T2], 0, 0, 0);
+            }
+        }
+    };
+    for (uint32_t pass = 0; pass < n_pass; pass += 2u) {
+        run_pass(pass, rawA);
+        if (pass == 4u) TRACEW(6);
+        if (pass + 1u < n_pass) run_pass(pass + 1u, rawB);
+    }
+    TRACEW(7);
+    /* ---- the partials: (m, l) per head, unnormalised rows in out ---- */
+#pragma unroll
+    for (uint32_t k = 0; k < TW; k++) {
+        const uint32_t t = t0 + k;
+        if (t >= n_tok || ps[k] > pe[k]) continue;
+        const uint32_t item = t * a.n_kvh + kh;
+        const float lw = pair32_sum(sum16(l_run[k]));
+        if (lane < gqa) stg((fv2 *)(a.band_ml + ((size_t)item * gqa + lane) * 2u), (fv2){m_run[k], lw});
+        float *orow = a.out + ((size_t)t * a.n_head + kh * gqa) * 256u;
+#pragma unroll
+        for (uint32_t T2 = 0; T2 < 16u; T2++) {
+            f4_t v;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) v[i] = add_ror8(acc[k][T2][i]);
+            if (c < gqa) stg((f4_t *)(orow + (size_t)c * 256u + 16u * T2 + 4u * jg), v);
+        }
+    }
 }
 
 /* Merge the S split partials of one (item, head): weights 2^(m_s - M) over
@@ -2038,6 +2441,16 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
     return pl;
 }
 
+/* The prefill band kernel (Q4KV_BAND=0 turns it off, for measurement). */
+static bool band_enabled(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_BAND");
+        v = (e && e[0] == '0') ? 0 : 1;
+    }
+    return v != 0;
+}
+
 /* A fused append + attention launch exists for this shape. */
 static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
     return kind == Q4KV_Q8 && hd == 256u && (gqa <= 8u || slab_takes(gqa, false));
@@ -2059,6 +2472,24 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         dim3 grid(S, ni);
         const bool prof = prof_armed();
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
+        /* prefill through the slab kernel (one split): the shared recent
+         * window of consecutive tokens goes to the band kernel first */
+        a.band_nb = nullptr;
+        a.band_ml = nullptr;
+        if (MODE == MODE_INDEXED && KIND == Q4KV_Q8 && pl.slab && S == 1u && gqa <= 8u &&
+            band_enabled() && pb.ptr && (size_t)ni * (1u + 2u * gqa) <= pb.cap && ni % a.n_kvh == 0u) {
+            AttnArgs ab = a;
+            ab.band_nb = (int32_t *)pb.ptr;
+            ab.band_ml = pb.ptr + ni;
+            ab.kv_base = ni / a.n_kvh; /* tokens */
+            ab.idx = a.idx + (size_t)(i0 / a.n_kvh) * a.tok_stride;
+            ab.q = a.q + (size_t)(i0 / a.n_kvh) * a.n_head * a.hd;
+            ab.out = a.out + (size_t)(i0 / a.n_kvh) * a.n_head * a.hd;
+            qsa_band_k<<<dim3((ni / a.n_kvh + BAND_TOK - 1u) / BAND_TOK, a.n_kvh), 64u * BAND_WAVES, 0,
+                         q4kv_stream>>>(ab);
+            a.band_nb = ab.band_nb - i0; /* indexed by the launch's item */
+            a.band_ml = ab.band_ml - (size_t)i0 * gqa * 2u;
+        }
         /* double-buffered rows pay when a workgroup walks three or more chunks
          * (prefill, batched decode of many sequences); with one or two (the
          * 12-layer step) the extra LDS traffic does not */
