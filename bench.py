@@ -156,7 +156,6 @@ class Bench:
         assert lib.q4_hip_h2d(self.d_step, C.addressof(step), C.sizeof(step))
         self.graphs = None
         self.bgraphs = None
-        self.pad = None
 
     def q_ptr(self, s, layer):
         return self.d_q + (s * self.L + layer) * QO_B
@@ -185,30 +184,6 @@ class Bench:
         if self.bgraphs is None:
             self.bgraphs = _graphs(self.lib, self._enqueue_batched, self.R)
         assert self.lib.q4_hip_graph_launch(self.bgraphs[s])
-
-    def kernel_time(self, rounds=8):
-        """Average duration of the fused step kernel from HIP events the
-        library records around it on its stream. Each round queues a 2 GiB
-        device copy first and all selection sets' steps behind it, so the
-        steps run back to back once the copy ends and host enqueue gaps do not
-        enter the event intervals."""
-        lib, rt = self.lib, self.rt
-        n = 2 << 30
-        if self.pad is None:
-            self.pad = (rt.alloc(n), rt.alloc(n))
-        tot_ms, n_tot = 0.0, 0
-        for i in range(rounds + 1):
-            assert lib.q4_hip_copy(self.pad[1], self.pad[0], n // 4)
-            assert lib.q4kv_prof_begin(self.R)
-            assert all(self._enqueue_batched(r) for r in range(self.R))
-            t = C.c_double()
-            k = lib.q4kv_prof_end(C.byref(t))
-            assert k == self.R, f"prof_end returned {k}"
-            if i:  # the first round warms up
-                tot_ms += t.value
-                n_tot += k
-        rt.sync()
-        return tot_ms / n_tot
 
     def _enqueue_sequential(self, s):
         lib = self.lib
@@ -380,11 +355,26 @@ def _time_direct(b, enqueue, n_sets, steps):
     return (time.perf_counter() - t0) / steps
 
 
+USE_GRAPHS = True  # --graphs 0: direct launches only (profiling runs)
+
+
 def _time_both(b, enqueue, n_sets, steps):
-    """(direct, graph) seconds per step."""
+    """(direct, graph) seconds per step (graph None with --graphs 0)."""
     t_d = _time_direct(b, enqueue, n_sets, steps)
-    t_g = _time_graphs(b, _graphs(b.lib, enqueue, n_sets), steps)
+    t_g = _time_graphs(b, _graphs(b.lib, enqueue, n_sets), steps) if USE_GRAPHS else None
     return t_d, t_g
+
+
+def _time_steps(b, enqueue, n_sets, steps):
+    """Seconds per step, replayed from captured graphs (the reference's decode
+    pattern) or, with --graphs 0, enqueued directly."""
+    if USE_GRAPHS:
+        return _time_graphs(b, _graphs(b.lib, enqueue, n_sets), steps)
+    return _time_direct(b, enqueue, n_sets, steps)
+
+
+def _us(t, div=1):
+    return None if t is None else round(t / div * 1e6, 3)
 
 
 def _fill(b, ptr, n_tok, kind, seed):
@@ -453,7 +443,7 @@ def config2(b, steps=200, sets=10):
         rt.free(p_)
     return {"what": "32 sequences (ctx log-uniform 8192-131072, seed 1236), one batched decode "
                     "step each: q8_0 append + sparse attention over 2x2051 positions",
-            "us_per_step": round(t * 1e6, 2), "graph_us_per_step": round(t_graph * 1e6, 2),
+            "us_per_step": round(t * 1e6, 2), "graph_us_per_step": _us(t_graph),
             "bytes_per_step": byts,
             "gbs": round(byts / t / 1e9, 1), "pct_of_peak": round(100 * byts / t / 1e9 / PEAK_GBS, 2),
             "steps": steps, "selection_sets": sets,
@@ -542,11 +532,10 @@ def config4(b, steps=100, sets=16, layers=12):
         sz = C.sizeof(q4kv.StepDesc)
         t, t_graph = _time_both(b, lambda r: lib.q4_hip_qsa_step_batch(
             dd + r * layers * sz, layers, N_HEAD, N_KVH, HD, 1.0 / 16, kind, WIDTH), sets, steps)
-        t, t_graph = t / layers, t_graph / layers
         byts = 2 * N_KVH * WIDTH * (bpt // N_KVH) + IDX_B + 2 * QO_B + 2 * N_KVH * HD * 4 + 2 * bpt
-        out[name] = {"us_per_layer": round(t * 1e6, 3),
-                     "graph_us_per_layer": round(t_graph * 1e6, 3), "bytes_per_layer": byts,
-                     "gbs": round(byts / t / 1e9, 1), "layers_per_step": layers,
+        out[name] = {"us_per_layer": _us(t, layers), "graph_us_per_layer": _us(t_graph, layers),
+                     "bytes_per_layer": byts,
+                     "gbs": round(byts * layers / t / 1e9, 1), "layers_per_step": layers,
                      "selection_sets": sets, "gathered_bytes_rotated": sets * layers * byts}
         for p_ in kcs + vcs + [dd]:
             rt.free(p_)
@@ -652,8 +641,7 @@ def config_prep(b, steps=200, sets=4, rot=64, base=1.0e7, eps=1.0e-6):
                    "heads (+ gates) and the 2 new key rows",
            "launches": {"fused": 2, "separate": 3 * L + 2}}
     for name, fn in (("fused", fused), ("separate", separate)):
-        graphs = _graphs(lib, fn, sets)
-        t = _time_graphs(b, graphs, steps) / L
+        t = _time_steps(b, fn, sets, steps) / L
         out[f"{name}_us_per_layer"] = round(t * 1e6, 3)
     for p_ in (qg, wq, wk, gbuf, qtmp, ktmp, dp, ds):
         rt.free(p_)
@@ -701,15 +689,13 @@ def config_out(b, steps=100, sets=4, n_embd=4096):
                    f"[{n_embd}][{ncols}], {wbytes} B per layer)",
            "launches": {"fused": 2, "separate": 2 + L}}
     for name, fn in (("fused", fused), ("separate", separate)):
-        graphs = _graphs(lib, fn, min(sets, b.R))
-        t = _time_graphs(b, graphs, steps) / L
+        t = _time_steps(b, fn, min(sets, b.R), steps) / L
         out[f"{name}_us_per_layer"] = round(t * 1e6, 3)
     # the GEMV alone: one launch per layer, W streamed from HBM (12 x 17.8 MB)
-    graphs = _graphs(lib, lambda r: all(lib.q4_hip_gemv_dd(8, ws[li], n_embd, ncols,
-                                                           b.d_out + li * QO_B,
-                                                           ys + li * n_embd * 4, 1.0)
-                                        for li in range(L)), 1)
-    t = _time_graphs(b, graphs, steps) / L
+    t = _time_steps(b, lambda r: all(lib.q4_hip_gemv_dd(8, ws[li], n_embd, ncols,
+                                                        b.d_out + li * QO_B,
+                                                        ys + li * n_embd * 4, 1.0)
+                                     for li in range(L)), 1, steps) / L
     out["gemv_us_per_layer"] = round(t * 1e6, 3)
     out["gemv_gbs"] = round((wbytes + ncols * 4 + n_embd * 4) / t / 1e9, 1)
     for p_ in ws + [ys, dd]:
@@ -746,7 +732,7 @@ def config_gqa12(b, steps=200, n_head=24):
         rt.free(p_)
     return {"what": f"{L}-layer decode step, {n_head} query heads / {N_KVH} KV heads "
                     f"(gqa {n_head // N_KVH}), same caches and selections as the headline",
-            "us_per_layer": round(t / L * 1e6, 3), "graph_us_per_layer": round(t_graph / L * 1e6, 3),
+            "us_per_layer": _us(t, L), "graph_us_per_layer": _us(t_graph, L),
             "bytes_per_layer": byts, "gbs": round(byts * L / t / 1e9, 1),
             "selection_sets": R}
 
@@ -837,12 +823,10 @@ def config_indexer(b, steps=100, layers=12):
     out = {"what": f"decode indexer, {layers} layers x 65536 visible blocks (ctx {CTX}), "
                    "4 heads x 128 dims, top-512 of 4-position blocks -> 2051 positions",
            "launches_per_layer": {"full": 5, "fused": 2, "batched": 2.0 / layers}}
-    graphs = _graphs(lib, batched, 2)
-    out["batched_us_per_layer"] = round(_time_graphs(b, graphs, steps) / layers * 1e6, 3)
+    out["batched_us_per_layer"] = round(_time_steps(b, batched, 2, steps) / layers * 1e6, 3)
     for name, parts in (("full", ("store", "prep", "score", "topk")), ("score", ("score",)),
                         ("topk", ("topk",)), ("fused", ("fused", "topk"))):
-        graphs = _graphs(lib, lambda r: step(parts), 2)
-        t = _time_graphs(b, graphs, steps) / layers
+        t = _time_steps(b, lambda r, parts=parts: step(parts), 2, steps) / layers
         out[f"{name}_us_per_layer"] = round(t * 1e6, 3)
     score_b = max_blocks * (IDX_DIM * 4 + 4) + IDX_HEADS * IDX_DIM * 4
     out["score_bytes_per_layer"] = score_b
@@ -939,6 +923,9 @@ def main():
     ap.add_argument("--sets", type=int, default=16)
     ap.add_argument("--mode", choices=["batched", "sequential", "both"], default="both")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--graphs", type=int, default=1,
+                    help="also time graph-replayed variants (0: direct launches only, as in "
+                         "profiling runs)")
     ap.add_argument("--configs", type=int, default=1,
                     help="also measure configs 2, 3 and 4 (0 to skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -947,6 +934,8 @@ def main():
                     help="only measure one of the extra configurations and print its JSON "
                          "(for profiling)")
     args = ap.parse_args()
+    global USE_GRAPHS
+    USE_GRAPHS = bool(args.graphs)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the QSA KV path runs on a single MI355X "
               "(no collectives); run with --gpus 1", file=sys.stderr)
@@ -969,11 +958,16 @@ def main():
     kern_ms = None
     if args.mode in ("batched", "both"):
         res["batched"] = b.timed(b.step_batched, args.steps, args.warmup)
-        res["batched_graph"] = b.timed(b.step_batched_graph, args.steps, args.warmup)
-        kern_ms = b.kernel_time()
+        if USE_GRAPHS:
+            res["batched_graph"] = b.timed(b.step_batched_graph, args.steps, args.warmup)
+        # the fused step kernel's duration, from HIP events the library
+        # records around each of its launches on its stream, over a second
+        # pass of the same timed steps
+        _, _, kern_ms = b.timed(b.step_batched, args.steps, args.warmup, prof=True)
     if args.mode in ("sequential", "both"):
         res["sequential"] = b.timed(b.step_sequential, args.steps, args.warmup)
-        res["sequential_graph"] = b.timed(b.step_sequential_graph, args.steps, args.warmup)
+        if USE_GRAPHS:
+            res["sequential_graph"] = b.timed(b.step_sequential_graph, args.steps, args.warmup)
     g_us, g_gbs = b.gather_ceiling()
     configs = None
     if args.configs:
@@ -1018,6 +1012,8 @@ def main():
                            "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4), "traffic": None,
                            "kernel": "qsa_q8d256_k<MODE_STEP>",
                            "kernel_us": round(kern_s * 1e3, 3),
+                           "kernel_us_source": "HIP events around each launch over a second "
+                                               "pass of the timed steps (library stream)",
                            "bytes_per_launch": L * SPLIT_KERNEL_B}
     if configs:
         out["configs"] = configs
