@@ -1627,40 +1627,57 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             /* ---- P.V over the 8 blocks: tiles 2b (even dims), 2b + 1 (odd) ---- */
             /* this lane's 8 positions: 4 jg .. 4 jg + 3, 16 + 4 jg .. 16 + 4 jg + 3 */
             const uint8_t *vp0 = vrow + (4u * jg) * ROWB, *vp1 = vrow + (16u + 4u * jg) * ROWB;
-#pragma unroll
-            for (uint32_t b = 0; b < 8u; b++) {
-                const uint8_t *s0 = vp0 + 34u * b, *s1 = vp1 + 34u * b;
+            /* block b's LDS operands: V scales of the lane's 8 positions, and
+             * the 16-bit V reads (dims 2c, 2c + 1) at those positions; block
+             * b + 1's are requested before block b is computed */
+            struct VOps {
+                uint32_t vw[4], x[8];
+            };
+            auto load_v = [&](uint32_t b, VOps &o) {
                 const uint2 va = *(const uint2 *)&vsT[slab][b][4u * jg];
                 const uint2 vb = *(const uint2 *)&vsT[slab][b][16u + 4u * jg];
-                const uint32_t vw[4] = {va.x, va.y, vb.x, vb.y};
+                o.vw[0] = va.x;
+                o.vw[1] = va.y;
+                o.vw[2] = vb.x;
+                o.vw[3] = vb.y;
+                const uint8_t *s0 = vp0 + 34u * b + 2u + 2u * c, *s1 = vp1 + 34u * b + 2u + 2u * c;
+#pragma unroll
+                for (uint32_t i = 0; i < 8u; i++)
+                    o.x[i] = *(const uint16_t *)((i < 4u ? s0 : s1) + (i & 3u) * ROWB);
+            };
+            VOps cur, nxt;
+            load_v(0u, cur);
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++) {
+                if (b + 1u < 8u) load_v(b + 1u, nxt);
+                __builtin_amdgcn_sched_barrier(0);
                 float u[8];
 #pragma unroll
                 for (uint32_t i = 0; i < 4u; i++) {
-                    u[2u * i] = __builtin_fmaf(P[2u * i], h2lo(vw[i]), 0.f);
-                    u[2u * i + 1u] = __builtin_fmaf(P[2u * i + 1u], h2hi(vw[i]), 0.f);
+                    u[2u * i] = __builtin_fmaf(P[2u * i], h2lo(cur.vw[i]), 0.f);
+                    u[2u * i + 1u] = __builtin_fmaf(P[2u * i + 1u], h2hi(cur.vw[i]), 0.f);
                 }
                 const u4_t bw = {split_pk(u[0], u[1], nsel), split_pk(u[2], u[3], nsel),
                                  split_pk(u[4], u[5], nsel), split_pk(u[6], u[7], nsel)};
                 const h8_t B = __builtin_bit_cast(h8_t, bw);
-                /* V^T: dims 2c, 2c + 1 of block b at the lane's 8 positions */
-                /* each 16-bit read holds dims 2c, 2c + 1 of one position; two
-                 * positions' even (odd) bytes go to one fp16 pair, which the
-                 * xor turns into 1024 + (b ^ 0x80) = 1152 + b */
+                /* V^T: each 16-bit read holds dims 2c, 2c + 1 of one position;
+                 * two positions' even (odd) bytes go to one fp16 pair, which
+                 * the xor turns into 1024 + (b ^ 0x80) = 1152 + b */
                 u4_t E, O;
 #pragma unroll
                 for (uint32_t k = 0; k < 4u; k++) {
-                    const uint8_t *vd = (k < 2u ? s0 : s1) + 2u + 2u * c + (2u * (k & 1u)) * ROWB;
-                    const uint32_t x0 = *(const uint16_t *)vd, x1 = *(const uint16_t *)(vd + ROWB);
-                    E[k] = __builtin_amdgcn_perm(x1, x0, 0x0C040C00u) ^ 0x64806480u;
-                    O[k] = __builtin_amdgcn_perm(x1, x0, 0x0C050C01u) ^ 0x64806480u;
+                    E[k] = __builtin_amdgcn_perm(cur.x[2u * k + 1u], cur.x[2u * k], 0x0C040C00u) ^ 0x64806480u;
+                    O[k] = __builtin_amdgcn_perm(cur.x[2u * k + 1u], cur.x[2u * k], 0x0C050C01u) ^ 0x64806480u;
                 }
                 acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     __builtin_bit_cast(h8_t, E), B, acc[2u * b], 0, 0, 0);
-                acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b], 0, 0, 0);
                 acc[2u * b + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     __builtin_bit_cast(h8_t, O), B, acc[2u * b + 1u], 0, 0, 0);
+                acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b], 0, 0, 0);
                 acc[2u * b + 1u] =
                     __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b + 1u], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                cur = nxt;
             }
         }
         if (HG > 1) __syncthreads(); /* the slab's rows are refilled next pass */
