@@ -2400,6 +2400,211 @@ static void choose_split(uint32_t n_items, uint32_t n_chunks, uint32_t gqa, bool
     if (S < 1u) S = 1u;
 }
 
+/* ---- shapes outside the MFMA kernels' tiling ----
+ * head_dim not a multiple of 32 (f16 / f32 caches, any hd <= 256), or more
+ * than 16 query heads per KV head (any width). The reference runs these on
+ * its one-block-per-head fallback (src/q4_rocm.cu:7286-7297); here one
+ * workgroup (4 x wave64) owns one (item, split, group of up to 8 query heads)
+ * and walks its list 256 entries at a time, 64 per wave:
+ *  - scores: lane = list entry; it reads its own K row element by element
+ *    (dequantised) against the group's query rows, held pre-scaled in LDS
+ *    and read as broadcasts;
+ *  - online softmax in base 2 per wave and head (wave max / sum over the
+ *    64 entries), the weights through LDS;
+ *  - P.V: lane = dimension (4 per lane), one V row per valid entry of the
+ *    wave's 64, coalesced across the wave;
+ *  - the four waves' (m, l, acc) merge in LDS; one split finalises (gate,
+ *    output), several write the partial rows qsa_comb_k merges (natural
+ *    column order). */
+constexpr uint32_t ANY_HEADS = 8u;
+
+__device__ static inline float ld_f16_g(const uint8_t *p) {
+    return __half2float(__ushort_as_half(ldg((const uint16_t *)p)));
+}
+
+template <int KIND>
+__device__ static inline float any_elem(const uint8_t *row, uint32_t d) {
+    if (KIND == Q4KV_F32) return ldg((const float *)row + d);
+    if (KIND == Q4KV_F16) return ld_f16_g(row + 2u * d);
+    const uint8_t *blk = row + 34u * (d >> 5);
+    return ld_f16_g(blk) * (float)(int8_t)ldg(blk + 2u + (d & 31u));
+}
+
+__device__ static inline float wave_sum64(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ static inline float wave_max64(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+template <int KIND, int MODE>
+__global__ __launch_bounds__(256) void qsa_any_k(AttnArgs a) {
+    constexpr uint32_t NH = ANY_HEADS;
+    __shared__ float qs[NH][256];
+    __shared__ float pw[4][64][NH];
+    __shared__ float wm[4][NH], wl[4][NH];
+    __shared__ float wacc[4][NH][256];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y, h0 = blockIdx.z * NH;
+    const uint32_t gqa = a.n_head / a.n_kvh, hd = a.hd, kh = item % a.n_kvh;
+    const uint32_t nh = gqa - h0 < NH ? gqa - h0 : NH;
+    const Item it = resolve_item<MODE>(a, item);
+    const uint32_t rowb = KIND == Q4KV_Q8 ? hd / 32u * 34u : hd * (KIND == Q4KV_F16 ? 2u : 4u);
+    const size_t rstride = (size_t)a.n_kvh * rowb;
+    const uint8_t *kbase = it.kc + (size_t)kh * rowb, *vbase = it.vc + (size_t)kh * rowb;
+
+    for (uint32_t e = tid; e < NH * 256u; e += 256u) {
+        const uint32_t h = e >> 8, d = e & 255u;
+        qs[h][d] = (h < nh && d < hd) ? ldg(it.q + (size_t)(h0 + h) * hd + d) * a.scale_log2 : 0.f;
+    }
+    __syncthreads();
+
+    const uint32_t n = it.n;
+    const uint32_t j0 = (uint32_t)(((uint64_t)s * n) / a.S);
+    const uint32_t j1 = (uint32_t)(((uint64_t)(s + 1u) * n) / a.S);
+    float m[NH], l[NH], acc[NH][4];
+#pragma unroll
+    for (uint32_t h = 0; h < NH; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) acc[h][i] = 0.f;
+    }
+    /* every wave runs the same iterations (the barriers stay matched) */
+    for (uint32_t c0 = j0; c0 < j1; c0 += 256u) {
+        const uint32_t j = c0 + 64u * wave + lane;
+        int32_t p = -1;
+        if (j < j1) p = it.list ? ldg(it.list + j) : (int32_t)j;
+        const bool ok = p >= 0 && (uint32_t)p < it.max_kv;
+        float sc[NH];
+#pragma unroll
+        for (uint32_t h = 0; h < NH; h++) sc[h] = 0.f;
+        if (ok) {
+            const uint8_t *kr = kbase + (size_t)p * rstride;
+            for (uint32_t d = 0; d < hd; d++) {
+                const float kv = any_elem<KIND>(kr, d);
+#pragma unroll
+                for (uint32_t h = 0; h < NH; h++) sc[h] = __builtin_fmaf(qs[h][d], kv, sc[h]);
+            }
+        }
+#pragma unroll
+        for (uint32_t h = 0; h < NH; h++) {
+            const float x = ok ? sc[h] : -INFINITY;
+            const float mn = fmaxf(m[h], wave_max64(x));
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            const float alpha = __builtin_amdgcn_exp2f(m[h] - ms);
+            const float pv = __builtin_amdgcn_exp2f(x - ms);
+            l[h] = l[h] * alpha + wave_sum64(pv);
+            m[h] = mn;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) acc[h][i] *= alpha;
+            pw[wave][lane][h] = pv;
+        }
+        __syncthreads();
+        uint64_t vm = __ballot(ok);
+        while (vm) {
+            const uint32_t jj = (uint32_t)__builtin_ctzll(vm);
+            vm &= vm - 1u;
+            const int32_t pj = __shfl(p, (int)jj);
+            const uint8_t *vr = vbase + (size_t)pj * rstride;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                const uint32_t d = lane + 64u * i;
+                if (d < hd) {
+                    const float vv = any_elem<KIND>(vr, d);
+#pragma unroll
+                    for (uint32_t h = 0; h < NH; h++)
+                        acc[h][i] = __builtin_fmaf(pw[wave][jj][h], vv, acc[h][i]);
+                }
+            }
+        }
+        __syncthreads(); /* pw is rewritten by the next iteration */
+    }
+
+    /* merge the four waves */
+#pragma unroll
+    for (uint32_t h = 0; h < NH; h++) {
+        if (lane == 0u) {
+            wm[wave][h] = m[h];
+            wl[wave][h] = l[h];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) wacc[wave][h][lane + 64u * i] = acc[h][i];
+    }
+    __syncthreads();
+    const bool fin = a.S == 1u;
+    float *pbase = fin ? nullptr : a.part + ((size_t)item * a.S + s) * gqa * PSTRIDE;
+    for (uint32_t e = tid; e < NH * 256u; e += 256u) {
+        const uint32_t h = e >> 8, d = e & 255u;
+        if (h >= nh || d >= hd) continue;
+        float M = -INFINITY;
+#pragma unroll
+        for (uint32_t w = 0; w < 4u; w++) M = fmaxf(M, wm[w][h]);
+        const float ms = M == -INFINITY ? 0.f : M;
+        float L = 0.f, x = 0.f;
+#pragma unroll
+        for (uint32_t w = 0; w < 4u; w++) {
+            const float f = __builtin_amdgcn_exp2f(wm[w][h] - ms);
+            L += f * wl[w][h];
+            x += f * wacc[w][h][d];
+        }
+        const uint32_t head = h0 + h;
+        if (fin) {
+            float r = L > 0.f ? x / L : 0.f;
+            if (it.gate) r *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)head * hd + d)));
+            stg(it.out + (size_t)head * hd + d, r);
+        } else {
+            stg(pbase + head * PSTRIDE + 2u + d, x);
+            if (d == 0u) {
+                stg(pbase + head * PSTRIDE, M);
+                stg(pbase + head * PSTRIDE + 1u, L);
+            }
+        }
+    }
+}
+
+/* The kernels above need hd a multiple of 32 and at most 16 query heads per
+ * KV head; every other shape runs qsa_any_k. */
+static bool any_shape(uint32_t hd, uint32_t gqa) { return (hd % 32u) != 0u || gqa > 16u; }
+
+/* qsa_any_k's split count: about split_target() workgroups, at most one
+ * split per 256 list entries, partials within cap floats. */
+static uint32_t any_splits(uint32_t n_items, uint32_t max_n, uint32_t gqa, bool have_part,
+                           size_t cap) {
+    const uint32_t hc = (gqa + ANY_HEADS - 1u) / ANY_HEADS;
+    const uint32_t n_iter = max_n ? (max_n + 255u) / 256u : 1u;
+    const uint64_t wgs = (uint64_t)n_items * hc;
+    uint32_t S = wgs >= split_target() ? 1u : (uint32_t)((split_target() + wgs - 1u) / wgs);
+    if (S > n_iter) S = n_iter;
+    if (S > COMB_MAXS) S = COMB_MAXS;
+    const size_t per = (size_t)gqa * PSTRIDE;
+    while (S > 1u && (size_t)n_items * S * per > cap) S--;
+    return have_part && S >= 1u ? S : 1u;
+}
+
+template <int KIND, int MODE>
+static bool launch_any(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa, PartBuf pb) {
+    const uint32_t hc = (gqa + ANY_HEADS - 1u) / ANY_HEADS;
+    const uint32_t S = any_splits(n_items, max_n, gqa, pb.ptr != nullptr, pb.cap);
+    a.S = S;
+    a.cps = 0u;
+    a.part = pb.ptr;
+    a.band_nb = nullptr;
+    a.band_ml = nullptr;
+    for (uint32_t i0 = 0; i0 < n_items; i0 += Q4KV_MAX_GRID_Y) {
+        const uint32_t ni = n_items - i0 < Q4KV_MAX_GRID_Y ? n_items - i0 : Q4KV_MAX_GRID_Y;
+        a.item0 = i0;
+        qsa_any_k<KIND, MODE><<<dim3(S, ni, hc), 256, 0, q4kv_stream>>>(a);
+        /* natural column order: the f32 instance's column map */
+        if (S > 1u) qsa_comb_k<Q4KV_F32, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
+    }
+    return hipGetLastError() == hipSuccess;
+}
+
 /* Which kernel runs a launch, and its split division. */
 struct Plan {
     bool slab;    /* qsa_slab_k (else qsa_q8d256_k / qsa_attn_k) */
@@ -2476,6 +2681,14 @@ static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
 template <int KIND, int MODE>
 static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa,
                         const OutProj *op = nullptr, PartBuf pb = lib_part()) {
+    if (any_shape(a.hd, gqa)) {
+        if constexpr (IS_STEP(MODE)) {
+            return false;
+        } else {
+            if (op) return false;
+            return launch_any<KIND, MODE>(a, n_items, max_n, gqa, pb);
+        }
+    }
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
     const Plan pl = plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap);
     if (IS_STEP(MODE) && !fast && !pl.slab) return false; /* the fused append needs these */
@@ -2549,11 +2762,12 @@ static bool launch_attn(int kind, const AttnArgs &a, uint32_t n_items, uint32_t 
     }
 }
 
-/* Shapes this kernel family supports: head_dim a multiple of 32 up to 256,
- * n_head a multiple of n_kvh with at most 16 query heads per KV head. */
+/* Shapes the attention entry points take: head_dim up to 256 (a multiple
+ * of 32 for q8_0, whose rows are 32-element blocks), n_head a multiple of
+ * n_kvh. */
 static bool shape_ok(uint32_t n_head, uint32_t n_kvh, uint32_t hd, int kind) {
-    if (!n_head || !n_kvh || !hd || hd > 256u || (hd % 32u) || (n_head % n_kvh)) return false;
-    if (n_head / n_kvh > 16u) return false;
+    if (!n_head || !n_kvh || !hd || hd > 256u || (n_head % n_kvh)) return false;
+    if (kind == Q4KV_Q8 && (hd % 32u)) return false;
     return kind >= Q4KV_F32 && kind <= Q4KV_Q8;
 }
 
@@ -2717,7 +2931,9 @@ extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uin
     const uint32_t gqa = n_head / n_kvh, n_items = n_seq * n_kvh;
     const bool have = q4kv_part != nullptr;
     const Plan pl =
-        step_fusable(kv_f16, hd, gqa)
+        any_shape(hd, gqa)
+            ? Plan{false, 1u, any_splits(n_items, max_n, gqa, have, q4kv_part_cap), 0u}
+        : step_fusable(kv_f16, hd, gqa)
             ? plan_launch<Q4KV_Q8, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
         : kv_f16 == Q4KV_F32
             ? plan_launch<Q4KV_F32, MODE_BATCH>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
