@@ -1762,6 +1762,298 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
 }
 
 /* ------------------------------------------------------------------------
+ * f16 cache, hd 256: the slab kernel's structure on plain fp16 MFMA. The
+ * cache values are fp16 already, so K rows are the score MFMA's A operand
+ * as stored (one 16-byte LDS read each) and V rows need only a 16-bit
+ * regroup; there are no block scales. Each wave owns a slab of 16 list
+ * entries per pass (4 slabs, or 2 slabs x 2 head groups for 9-16 query
+ * heads per KV head):
+ *  - scores S^T (16 positions x 8 heads hi | lo) = K (16 x 256) . Q^T over
+ *    eight v_mfma_f32_16x16x32_f16, Q split hi/lo (fp16 x 2, ~22 bits);
+ *  - the softmax weights P^T come out of the score tile in the lane layout
+ *    the P.V B operand needs (split hi/lo in place);
+ *  - O^T (dims x heads) += V^T . P^T over sixteen v_mfma_f32_16x16x16_f16:
+ *    per 32-dim block, four 32-bit reads (dims 2c, 2c + 1 at the lane's
+ *    four positions) regroup into the even-dim and odd-dim operands.
+ * Rows are 512 bytes in HBM and 528 in LDS (one 16-byte pad keeps the
+ * 16-row operand reads off a single bank group); padding entries are never
+ * fetched and their V rows are zeroed in LDS. MODE_STEP appends the token's
+ * K/V rows (fp16, round to nearest even, as q4_hip_kv_append_d) from split
+ * 0 and patches the LDS rows of any slab that lists the new position. */
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+constexpr uint32_t H16_SL = 16;  /* list entries per slab */
+
+static bool h16_enabled(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_H16");
+        v = (e && e[0] == '0') ? 0 : 1;
+    }
+    return v != 0;
+}
+
+template <int MODE, int HG>
+__global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
+    constexpr uint32_t SL = H16_SL, ROWB = 528, NCH = 33;
+    constexpr uint32_t NSLAB = 4u / HG, NE = NSLAB * SL;
+    constexpr uint32_t RBYTES = 2u * NE * ROWB;
+    constexpr uint32_t MBYTES = 4u * 16u * 8u * 20u * 4u; /* merge: [wave][tile][head][20] */
+    __shared__ __attribute__((aligned(16))) uint8_t rows[RBYTES > MBYTES ? RBYTES : MBYTES];
+    /* Q^T operands [head group][block][k-group][column][8 fp16] */
+    __shared__ __attribute__((aligned(16))) uint16_t qB[HG][8][4][16][8];
+    __shared__ float s_m[4][8], s_l[4][8];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t slab = wave / HG, hg = wave % HG;
+    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
+    const Item it = resolve_item<MODE>(a, item);
+    const uint32_t c = lane & 15u, jg = lane >> 4;
+    const float nsel = c >= 8u ? -1.f : 0.f;
+    const size_t rstride = (size_t)a.n_kvh * 512u;
+    const uint8_t *kbase = it.kc + (size_t)kh * 512u, *vbase = it.vc + (size_t)kh * 512u;
+    uint8_t *const krow = rows + slab * SL * ROWB;
+    uint8_t *const vrow = rows + NE * ROWB + slab * SL * ROWB;
+    const uint32_t n = it.n;
+    const uint32_t j0 = (uint32_t)(((uint64_t)s * n) / a.S);
+    const uint32_t j1 = (uint32_t)(((uint64_t)(s + 1u) * n) / a.S);
+    const uint32_t n_pass = j1 > j0 ? (j1 - j0 + NE - 1u) / NE : 0u;
+
+    /* lane l's list entry: slab position l & 15 */
+    int32_t raw = -1;
+    {
+        const uint32_t e = j0 + slab * SL + c;
+        if (e < j1) raw = it.list ? ldg(it.list + e) : (int32_t)e;
+    }
+    /* MODE_STEP: lane l holds dims 4 l .. 4 l + 3 of the new K and V rows,
+     * as fp16 */
+    uint32_t nk2[2] = {0u, 0u}, nv2[2] = {0u, 0u};
+    if (IS_STEP(MODE)) {
+        const f4_t k4 = ldg((const f4_t *)(it.knew + 4u * lane));
+        const f4_t v4 = ldg((const f4_t *)(it.vnew + 4u * lane));
+        auto h2 = [](float x, float y) {
+            return (uint32_t)__half_as_ushort(__float2half_rn(x)) |
+                   ((uint32_t)__half_as_ushort(__float2half_rn(y)) << 16);
+        };
+        nk2[0] = h2(k4[0], k4[1]);
+        nk2[1] = h2(k4[2], k4[3]);
+        nv2[0] = h2(v4[0], v4[1]);
+        nv2[1] = h2(v4[2], v4[3]);
+    }
+    /* this thread's share of the Q operands: head slot hh of head group k,
+     * block b, k-group kg (dims 32 b + 8 kg .. + 7) */
+    float qx[HG][8];
+    const uint32_t t_kg = tid & 3u, t_b = (tid >> 2) & 7u, t_hh = tid >> 5;
+#pragma unroll
+    for (uint32_t k = 0; k < HG; k++) {
+        const uint32_t h = 8u * k + t_hh;
+        const float *qr = it.q + (size_t)(h < gqa ? h : 0u) * 256u + 32u * t_b + 8u * t_kg;
+        const f4_t x0 = ldg((const f4_t *)qr), x1 = ldg((const f4_t *)(qr + 4));
+        const float sc = h < gqa ? a.scale_log2 : 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            qx[k][i] = x0[i] * sc;
+            qx[k][4u + i] = x1[i] * sc;
+        }
+    }
+
+    /* issue pass p: the slab's K/V rows by DMA (16 x 33 sixteen-byte slots
+     * per cache, slot u * 64 + lane, row = slot / 33; slot 32 of a row is
+     * its pad). Padding entries are not fetched. Returns whether the slab
+     * holds any valid position. */
+    auto issue = [&](uint32_t pass, int32_t &pos) -> bool {
+        const uint32_t e0 = j0 + pass * NE + slab * SL;
+        const uint32_t ne = e0 < j1 ? min(SL, j1 - e0) : 0u;
+        pos = (raw >= 0 && (uint32_t)raw < it.max_kv && c < ne) ? raw : -1;
+        const bool any = __ballot(pos >= 0) != 0u;
+        if (hg == 0u && any) {
+#pragma unroll
+            for (uint32_t u = 0; u < 9u; u++) {
+                const uint32_t e = u * 64u + lane;
+                const uint32_t r = e / NCH, q = e - r * NCH;
+                const int32_t pr = __builtin_amdgcn_ds_bpermute((int)((r & 15u) * 4u), pos);
+                const size_t off = (size_t)(pr < 0 ? 0 : pr) * rstride + q * 16u;
+                if (r < SL && q < 32u && pr >= 0) {
+                    dma16(kbase + off, krow + u * 1024u);
+                    dma16(vbase + off, vrow + u * 1024u);
+                }
+            }
+        }
+        return any;
+    };
+    int32_t pos = -1;
+    bool any = n_pass > 0u ? issue(0u, pos) : false;
+
+    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
+        stg((u2_t *)(kbase + (size_t)it.pos_new * rstride + 8u * lane), (u2_t){nk2[0], nk2[1]});
+        stg((u2_t *)(vbase + (size_t)it.pos_new * rstride + 8u * lane), (u2_t){nv2[0], nv2[1]});
+    }
+
+    /* ---- Q^T operands, built once per workgroup ---- */
+#pragma unroll
+    for (uint32_t k = 0; k < HG; k++) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            hw[i] = pkrtz(qx[k][2u * i], qx[k][2u * i + 1u]);
+            lw[i] = pkrtz(qx[k][2u * i] - h2lo(hw[i]), qx[k][2u * i + 1u] - h2hi(hw[i]));
+        }
+        *(u4_t *)&qB[k][t_b][t_kg][t_hh][0] = (u4_t){hw[0], hw[1], hw[2], hw[3]};
+        *(u4_t *)&qB[k][t_b][t_kg][t_hh + 8u][0] = (u4_t){lw[0], lw[1], lw[2], lw[3]};
+    }
+    __syncthreads();
+
+    float m_run = -INFINITY, l_run = 0.f;
+    f4_t acc[16];
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; t++) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    const uint16_t *const qBw = &qB[hg][0][jg][c][0];
+
+    for (uint32_t pass = 0; pass < n_pass; pass++) {
+        if (pass > 0u) any = issue(pass, pos);
+        raw = -1;
+        {
+            const uint32_t e = j0 + (pass + 1u) * NE + slab * SL + c;
+            if (pass + 1u < n_pass && e < j1) raw = it.list ? ldg(it.list + e) : (int32_t)e;
+        }
+        /* valid positions of the slab (bit p: entry p) */
+        const uint32_t vmask = (uint32_t)__ballot(pos >= 0) & 0xFFFFu;
+        __builtin_amdgcn_s_waitcnt(0);
+        if (HG > 1) __syncthreads(); /* the head-group waves share the slab's rows */
+        if (hg == 0u && any) {
+            /* padding entries: zero V rows (their weights are 0; stale LDS
+             * must not turn that into NaN) */
+            uint32_t padm = ~vmask & 0xFFFFu;
+            while (padm) {
+                const uint32_t r = (uint32_t)__builtin_ctz(padm);
+                padm &= padm - 1u;
+                if (lane < 32u) *(u4_t *)(vrow + r * ROWB + 16u * lane) = (u4_t){0u, 0u, 0u, 0u};
+            }
+            if (IS_STEP(MODE)) {
+                /* rows at the appended position take the new token's bytes */
+                uint32_t hit = (uint32_t)__ballot(lane < 16u && pos >= 0 &&
+                                                  (uint32_t)pos == it.pos_new);
+                while (hit) {
+                    const uint32_t r = (uint32_t)__builtin_ctz(hit);
+                    hit &= hit - 1u;
+                    *(u2_t *)(krow + r * ROWB + 8u * lane) = (u2_t){nk2[0], nk2[1]};
+                    *(u2_t *)(vrow + r * ROWB + 8u * lane) = (u2_t){nv2[0], nv2[1]};
+                }
+            }
+        }
+        if (HG > 1) __syncthreads();
+        if (any) {
+            /* ---- scores: S^T (positions x [heads hi | heads lo]) ---- */
+            f4_t S = {0.f, 0.f, 0.f, 0.f};
+            const uint8_t *kr = krow + c * ROWB + 16u * jg;
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++) {
+                const h8_t A = *(const h8_t *)(kr + 64u * b);
+                const h8_t B = *(const h8_t *)(qBw + b * 4u * 16u * 8u);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, S, 0, 0, 0);
+            }
+            /* ---- softmax over the slab (base 2; scores already scaled) ---- */
+            float T[4];
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                const float x = add_ror8(S[i]);
+                T[i] = (vmask >> (4u * jg + i)) & 1u ? x : -INFINITY;
+            }
+            float mx = fmax2(fmax2(T[0], T[1]), fmax2(T[2], T[3]));
+            mx = max32(max16(mx));
+            const float mn = fmax2(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+            const bool grew = mn > m_run;
+            m_run = mn;
+            float P[4];
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) P[i] = __builtin_amdgcn_exp2f(T[i] - mn);
+            l_run = l_run * alpha + ((P[0] + P[1]) + (P[2] + P[3]));
+            if (pass > 0u && __ballot(grew) != 0u) {
+#pragma unroll
+                for (uint32_t t = 0; t < 16u; t++) acc[t] *= alpha;
+            }
+            /* P^T operand: the lane's four positions, hi (columns < 8) or
+             * lo (columns >= 8) */
+            const h4_t Bp = __builtin_bit_cast(
+                h4_t, (u2_t){split_pk(P[0], P[1], nsel), split_pk(P[2], P[3], nsel)});
+            /* ---- P.V: per 32-dim block b, tiles 2b (even dims), 2b + 1 (odd) ---- */
+            const uint8_t *vr = vrow + (4u * jg) * ROWB + 4u * c;
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++) {
+                uint32_t x[4];
+#pragma unroll
+                for (uint32_t i = 0; i < 4u; i++) x[i] = *(const uint32_t *)(vr + i * ROWB + 64u * b);
+                const u2_t E = {__builtin_amdgcn_perm(x[1], x[0], 0x05040100u),
+                                 __builtin_amdgcn_perm(x[3], x[2], 0x05040100u)};
+                const u2_t O = {__builtin_amdgcn_perm(x[1], x[0], 0x07060302u),
+                                 __builtin_amdgcn_perm(x[3], x[2], 0x07060302u)};
+                acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    __builtin_bit_cast(h4_t, E), Bp, acc[2u * b], 0, 0, 0);
+                acc[2u * b + 1u] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    __builtin_bit_cast(h4_t, O), Bp, acc[2u * b + 1u], 0, 0, 0);
+            }
+        }
+        if (HG > 1) __syncthreads(); /* the slab's rows are refilled next pass */
+    }
+
+    /* ---- merge the waves: (m, l) per head, acc to the common max ---- */
+    const float lw = pair32_sum(sum16(l_run));
+    if (lane < 8u) {
+        s_m[wave][lane] = m_run;
+        s_l[wave][lane] = lw;
+    }
+    __syncthreads(); /* every wave is done with the rows: the merge reuses them */
+    float *const mrg = (float *)rows;
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; t++) {
+        f4_t v;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) v[i] = add_ror8(acc[t][i]);
+        if (c < 8u) *(f4_t *)(mrg + ((wave * 16u + t) * 8u + c) * 20u + 4u * jg) = v;
+    }
+    __syncthreads();
+    /* output column 16 t + r of a head is dim 32 (t >> 1) + 2 r + (t & 1):
+     * the q8_0 kernels' column order, so qsa_comb_k<Q4KV_Q8> merges splits */
+#pragma unroll
+    for (uint32_t k = 0; k < 2u * HG; k++) {
+        const uint32_t task = tid + 256u * k;
+        const uint32_t thg = task >> 9, hh = (task >> 6) & 7u, t = (task >> 2) & 15u, jq = task & 3u;
+        const uint32_t g = 8u * thg + hh;
+        if (g >= gqa) continue;
+        const uint32_t col = 16u * t + 4u * jq;
+        float Mh = -INFINITY;
+#pragma unroll
+        for (uint32_t w = thg; w < 4u; w += HG) Mh = fmax2(Mh, s_m[w][hh]);
+        float L = 0.f;
+        f4_t v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t w = thg; w < 4u; w += HG) {
+            const float mw = s_m[w][hh];
+            const float fw = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - Mh);
+            L += fw * s_l[w][hh];
+            v += fw * *(const f4_t *)(mrg + ((w * 16u + t) * 8u + hh) * 20u + 4u * jq);
+        }
+        if (a.S == 1u) {
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                const uint32_t d = col_dim<Q4KV_Q8>(col + i);
+                float r = v[i] * inv;
+                if (it.gate) r *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)g * 256u + d)));
+                stg(it.out + (size_t)g * 256u + d, r);
+            }
+        } else {
+            float *pb = a.part + ((size_t)item * a.S + s) * gqa * PSTRIDE + (size_t)g * PSTRIDE;
+            stg((fv2 *)(pb + 2u + col), (fv2){v[0], v[1]});
+            stg((fv2 *)(pb + 4u + col), (fv2){v[2], v[3]});
+            if (t == 0u && jq == 0u) stg((fv2 *)pb, (fv2){Mh, L});
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------
  * Prefill band kernel: the recent window that consecutive prefill tokens'
  * lists share, as dense MFMA tiles. A token's band is the longest run of
  * consecutive positions that ends its list (the causal recent window); the
@@ -2608,8 +2900,9 @@ static bool launch_any(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gq
 /* Which kernel runs a launch, and its split division. */
 struct Plan {
     bool slab;    /* qsa_slab_k (else qsa_q8d256_k / qsa_attn_k) */
-    uint32_t hg;  /* slab kernel: head groups of 8 */
+    uint32_t hg;  /* slab kernels: head groups of 8 */
     uint32_t S, cps;
+    bool h16;     /* qsa_h16_k (f16 cache, hd 256) */
 };
 
 /* The slab kernel takes q8_0 / hd 256 shapes with 9 to 16 query heads per KV
@@ -2638,7 +2931,26 @@ static bool slab_takes(uint32_t gqa, bool prefill_sized) {
 template <int KIND, int MODE>
 static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t gqa,
                         bool have_part, size_t cap) {
-    Plan pl = {false, 1u, 1u, 1u};
+    Plan pl = {false, 1u, 1u, 1u, false};
+    if (KIND == Q4KV_F16 && hd == 256u && gqa <= 16u && h16_enabled()) {
+        /* one pass of every wave per split; prefill-sized launches stream
+         * their passes through fewer splits */
+        const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 4u / hg * H16_SL;
+        const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
+        uint32_t S = (uint64_t)n_items * s_full <= SLAB_MAX_WG ? s_full
+                     : n_items >= SLAB_MAX_WG                  ? 1u
+                                                               : SLAB_MAX_WG / n_items;
+        if (S < 1u) S = 1u;
+        if (S > COMB_MAXS) S = COMB_MAXS;
+        const size_t per = (size_t)gqa * PSTRIDE;
+        while (S > 1u && (size_t)n_items * S * per > cap) S--;
+        if (!have_part) S = 1u;
+        pl.h16 = true;
+        pl.hg = hg;
+        pl.S = S;
+        pl.cps = 0u;
+        return pl;
+    }
     const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
     const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
     const bool prefill_sized = (uint64_t)n_items * s_full > SLAB_MAX_WG;
@@ -2675,6 +2987,7 @@ static bool band_enabled(void) {
 
 /* A fused append + attention launch exists for this shape. */
 static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
+    if (kind == Q4KV_F16) return hd == 256u && gqa <= 16u && h16_enabled();
     return kind == Q4KV_Q8 && hd == 256u && (gqa <= 8u || slab_takes(gqa, false));
 }
 
@@ -2691,7 +3004,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
     }
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
     const Plan pl = plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap);
-    if (IS_STEP(MODE) && !fast && !pl.slab) return false; /* the fused append needs these */
+    if (IS_STEP(MODE) && !fast && !pl.slab && !pl.h16) return false; /* the fused append needs these */
     const uint32_t S = pl.S, cps = pl.cps;
     a.S = S;
     a.cps = cps;
@@ -2723,7 +3036,11 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         /* double-buffered rows pay when a workgroup walks three or more chunks
          * (prefill, batched decode of many sequences); with one or two (the
          * 12-layer step) the extra LDS traffic does not */
-        if (pl.slab && pl.hg == 1u)
+        if (pl.h16 && pl.hg == 1u)
+            qsa_h16_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (pl.h16)
+            qsa_h16_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (pl.slab && pl.hg == 1u)
             qsa_slab_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (pl.slab)
             qsa_slab_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
@@ -2738,7 +3055,11 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         else
             qsa_attn_k<KIND, IS_STEP(MODE) ? MODE_BATCH : MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n++ + 1], q4kv_stream);
-        if (S > 1u && !op) qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
+        /* qsa_h16_k writes the q8_0 kernels' column order */
+        if (S > 1u && !op && pl.h16)
+            qsa_comb_k<Q4KV_Q8, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
+        else if (S > 1u && !op)
+            qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
     }
     if (op) {
         if (!fast && !pl.slab) return false;
@@ -2864,6 +3185,8 @@ static bool step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32_t n
     a.seqs = (const q4kv_seq_desc *)d_descs;
     a.desc_stride = sizeof(q4kv_step_desc);
     const uint32_t gqa = n_head / n_kvh;
+    if (step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F16)
+        return launch_kind<Q4KV_F16, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, nullptr, pb);
     if (step_fusable(kv_f16, hd, gqa))
         return launch_kind<Q4KV_Q8, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, nullptr, pb);
     /* other widths and shapes: the append launch, then the attention */
@@ -2933,6 +3256,8 @@ extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uin
     const Plan pl =
         any_shape(hd, gqa)
             ? Plan{false, 1u, any_splits(n_items, max_n, gqa, have, q4kv_part_cap), 0u}
+        : step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F16
+            ? plan_launch<Q4KV_F16, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
         : step_fusable(kv_f16, hd, gqa)
             ? plan_launch<Q4KV_Q8, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
         : kv_f16 == Q4KV_F32

@@ -124,10 +124,11 @@ def test_step_batch_q8_matches_append_then_decode(rt, oracle, n_seq):
     _check(rt, oracle, items, ctx, q4kv.KV_Q8, what=f"q8 {n_seq} layers")
 
 
-def test_step_batch_position_anywhere_in_list(rt, oracle):
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+def test_step_batch_position_anywhere_in_list(rt, oracle, kind):
     """The new position listed first, in a middle chunk and twice, or not at
     all (then only the cache write shows it)."""
-    rng = np.random.default_rng(901)
+    rng = np.random.default_rng(901 + kind)
     ctx = 8192
 
     def sel_of(rng, s, pos):
@@ -140,42 +141,46 @@ def test_step_batch_position_anywhere_in_list(rt, oracle):
             base[:, 70] = pos                     # twice, two chunks
             base[:, 2000] = pos
         return base                               # s == 3: not listed
-    items, _ = _case(rng, oracle, 4, ctx, q4kv.KV_Q8, lambda s: 5000 + 37 * s, sel_of)
-    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what="position anywhere")
+    items, _ = _case(rng, oracle, 4, ctx, kind, lambda s: 5000 + 37 * s, sel_of)
+    _check(rt, oracle, items, ctx, kind, what=f"position anywhere, width {kind}")
 
 
-def test_step_batch_dense_items(rt, oracle):
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+def test_step_batch_dense_items(rt, oracle, kind):
     """Dense items (no list): positions 0 .. pos, the new one last."""
-    rng = np.random.default_rng(902)
+    rng = np.random.default_rng(902 + kind)
     ctx = 4096
-    items, _ = _case(rng, oracle, 3, ctx, q4kv.KV_Q8, lambda s: 1000 + 1500 * s, _sel_kv)
-    _check(rt, oracle, items, ctx, q4kv.KV_Q8, dense=True, what="dense")
+    items, _ = _case(rng, oracle, 3, ctx, kind, lambda s: 1000 + 1500 * s, _sel_kv)
+    _check(rt, oracle, items, ctx, kind, dense=True, what=f"dense, width {kind}")
 
 
 @pytest.mark.parametrize("kind", [q4kv.KV_F16, q4kv.KV_F32])
 def test_step_batch_other_widths(rt, oracle, kind):
-    """f16 / f32 caches take the append launch then the attention launch."""
+    """f16 caches take the fused launch (append inside the attention), f32
+    caches the append launch then the attention launch."""
     rng = np.random.default_rng(903 + kind)
     ctx = 4096
     items, _ = _case(rng, oracle, 3, ctx, kind, lambda s: ctx - 1 - 300 * s, _sel_kv)
     _check(rt, oracle, items, ctx, kind, what=f"width {kind}")
 
 
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
 @pytest.mark.parametrize("n_head", [24, 32, 18])
-def test_step_batch_q8_more_heads_per_kv_head(rt, oracle, n_head):
+def test_step_batch_more_heads_per_kv_head(rt, oracle, n_head, kind):
     """The production layout (24 query heads over 2 KV heads, 12 per KV head),
     16 per KV head, and an odd 9: the fused step of two head groups against
     append + batched decode, and against the oracle."""
-    rng = np.random.default_rng(950 + n_head)
+    rng = np.random.default_rng(950 + n_head + 100 * kind)
     ctx = 16384
-    items, _ = _case(rng, oracle, 12, ctx, q4kv.KV_Q8, lambda s: ctx - 1 - 300 * s, _sel_kv,
+    items, _ = _case(rng, oracle, 12, ctx, kind, lambda s: ctx - 1 - 300 * s, _sel_kv,
                      n_head=n_head)
-    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what=f"q8 12 layers, {n_head} heads")
+    _check(rt, oracle, items, ctx, kind, what=f"width {kind}, 12 layers, {n_head} heads")
 
 
-def test_step_batch_more_heads_position_anywhere(rt, oracle):
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+def test_step_batch_more_heads_position_anywhere(rt, oracle, kind):
     """24 heads: the new position first, in a middle split, twice, or not at all."""
-    rng = np.random.default_rng(960)
+    rng = np.random.default_rng(960 + kind)
     ctx = 8192
 
     def sel_of(rng, s, pos):
@@ -188,5 +193,5 @@ def test_step_batch_more_heads_position_anywhere(rt, oracle):
             base[:, 70] = pos
             base[:, 2000] = pos
         return base
-    items, _ = _case(rng, oracle, 4, ctx, q4kv.KV_Q8, lambda s: 5000 + 37 * s, sel_of, n_head=24)
-    _check(rt, oracle, items, ctx, q4kv.KV_Q8, what="24 heads, position anywhere")
+    items, _ = _case(rng, oracle, 4, ctx, kind, lambda s: 5000 + 37 * s, sel_of, n_head=24)
+    _check(rt, oracle, items, ctx, kind, what=f"24 heads, position anywhere, width {kind}")
