@@ -2054,6 +2054,185 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
 }
 
 /* ------------------------------------------------------------------------
+ * f32 cache, hd 256: rows of 1 KB, contracted on fp32 MFMA
+ * (v_mfma_f32_16x16x4_f32: exact fp32 products, no hi/lo split). A 64-entry
+ * pass of K and V rows would need 128 KB of LDS, so each wave loads its 16
+ * entries' rows straight into registers (16 + 16 sixteen-byte loads per
+ * lane, all issued before the first is used) and the four waves never
+ * synchronise inside the loop:
+ *  - scores S^T (16 positions x 16 heads) = K . Q^T over 64 MFMAs; lane
+ *    (c, g) holds K[position c][16 m + 4 g .. + 3] for m < 16, and the
+ *    matching Q^T operands come from LDS;
+ *  - the softmax weights are the P.V B operand in place (lane (c, g),
+ *    MFMA i: position 4 g + i, head c);
+ *  - O^T (16 tiles of 16 dims x 16 heads) += V^T . P^T over 64 MFMAs; lane
+ *    (c, g) holds V[position 4 g + i][64 t' + 4 c .. + 3] for i, t' < 4, so
+ *    tile 4 t' + u has dims 64 t' + 4 c + u on its rows.
+ * Padding entries load nothing (zero rows, weight 0). MODE_STEP appends the
+ * token's rows (fp32, as stored) from split 0 and substitutes them in the
+ * registers of any lane whose entry is the new position. */
+static bool f32w_enabled(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_F32W");
+        v = (e && e[0] == '0') ? 0 : 1;
+    }
+    return v != 0;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void qsa_f32w_k(AttnArgs a) {
+    constexpr uint32_t SL = 16u, NE = 64u;
+    /* the Q^T operands [m][g][head][4] during the loop; the waves' output
+     * tiles [wave][tile][lane][4] for the merge */
+    __shared__ __attribute__((aligned(16))) float lds[4u * 16u * 64u * 4u];
+    __shared__ float s_m[4][16], s_l[4][16];
+    float(*qT)[4][16][4] = (float(*)[4][16][4])lds;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
+    const Item it = resolve_item<MODE>(a, item);
+    const uint32_t c = lane & 15u, jg = lane >> 4;
+    const size_t rstride = (size_t)a.n_kvh * 1024u;
+    const uint8_t *kbase = it.kc + (size_t)kh * 1024u, *vbase = it.vc + (size_t)kh * 1024u;
+    const uint32_t n = it.n;
+    const uint32_t j0 = (uint32_t)(((uint64_t)s * n) / a.S);
+    const uint32_t j1 = (uint32_t)(((uint64_t)(s + 1u) * n) / a.S);
+    const uint32_t n_pass = j1 > j0 ? (j1 - j0 + NE - 1u) / NE : 0u;
+
+    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
+        stg((f4_t *)(kbase + (size_t)it.pos_new * rstride) + lane, ldg((const f4_t *)it.knew + lane));
+        stg((f4_t *)(vbase + (size_t)it.pos_new * rstride) + lane, ldg((const f4_t *)it.vnew + lane));
+    }
+    for (uint32_t e = tid; e < 16u * 256u; e += 256u) {
+        const uint32_t h = e >> 8, d = e & 255u;
+        qT[d >> 4][(d >> 2) & 3u][h][d & 3u] =
+            h < gqa ? ldg(it.q + (size_t)h * 256u + d) * a.scale_log2 : 0.f;
+    }
+    __syncthreads();
+
+    float m_run = -INFINITY, l_run = 0.f;
+    f4_t acc[16];
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; t++) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
+    const f4_t z4 = {0.f, 0.f, 0.f, 0.f};
+
+    for (uint32_t pass = 0; pass < n_pass; pass++) {
+        /* lane l's entry: slab position l & 15 */
+        const uint32_t e = j0 + pass * NE + wave * SL + c;
+        int32_t pk = -1;
+        if (e < j1) pk = it.list ? ldg(it.list + e) : (int32_t)e;
+        if (pk >= 0 && (uint32_t)pk >= it.max_kv) pk = -1;
+        const uint32_t vmask = (uint32_t)__ballot(pk >= 0) & 0xFFFFu;
+        if (!vmask) continue; /* wave-uniform */
+        int32_t pv[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) pv[i] = __shfl(pk, (int)(4u * jg + i));
+        /* K: position c, dims 16 m + 4 jg .. + 3; V: positions 4 jg + i,
+         * dims 64 t + 4 c .. + 3 */
+        f4_t kr[16], vr[4][4];
+        const f4_t *kp = (const f4_t *)(kbase + (size_t)(pk < 0 ? 0 : pk) * rstride) + jg;
+#pragma unroll
+        for (uint32_t m = 0; m < 16u; m++) kr[m] = pk >= 0 ? ldg(kp + 4u * m) : z4;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            const f4_t *vp = (const f4_t *)(vbase + (size_t)(pv[i] < 0 ? 0 : pv[i]) * rstride) + c;
+#pragma unroll
+            for (uint32_t t = 0; t < 4u; t++) vr[i][t] = pv[i] >= 0 ? ldg(vp + 16u * t) : z4;
+        }
+        if (IS_STEP(MODE)) {
+            if (pk >= 0 && (uint32_t)pk == it.pos_new) {
+#pragma unroll
+                for (uint32_t m = 0; m < 16u; m++) kr[m] = ldg((const f4_t *)it.knew + 4u * m + jg);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++)
+                if (pv[i] >= 0 && (uint32_t)pv[i] == it.pos_new) {
+#pragma unroll
+                    for (uint32_t t = 0; t < 4u; t++) vr[i][t] = ldg((const f4_t *)it.vnew + 16u * t + c);
+                }
+        }
+        /* ---- scores ---- */
+        f4_t S = z4;
+#pragma unroll
+        for (uint32_t m = 0; m < 16u; m++) {
+            const f4_t qb = *(const f4_t *)&qT[m][jg][c][0];
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++)
+                S = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[m][i], qb[i], S, 0, 0, 0);
+        }
+        /* ---- softmax (base 2; scores already scaled) ---- */
+        float T[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) T[i] = (vmask >> (4u * jg + i)) & 1u ? S[i] : -INFINITY;
+        float mx = fmax2(fmax2(T[0], T[1]), fmax2(T[2], T[3]));
+        mx = max32(max16(mx));
+        const float mn = fmax2(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+        const bool grew = mn > m_run;
+        m_run = mn;
+        float P[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) P[i] = __builtin_amdgcn_exp2f(T[i] - mn);
+        l_run = l_run * alpha + ((P[0] + P[1]) + (P[2] + P[3]));
+        if (__ballot(grew) != 0u) {
+#pragma unroll
+            for (uint32_t t = 0; t < 16u; t++) acc[t] *= alpha;
+        }
+        /* ---- P.V ---- */
+#pragma unroll
+        for (uint32_t t = 0; t < 4u; t++)
+#pragma unroll
+            for (uint32_t u = 0; u < 4u; u++)
+#pragma unroll
+                for (uint32_t i = 0; i < 4u; i++)
+                    acc[4u * t + u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[i][t][u], P[i],
+                                                                          acc[4u * t + u], 0, 0, 0);
+    }
+
+    /* ---- merge the waves ---- */
+    const float lw = pair32_sum(sum16(l_run));
+    if (lane < 16u) {
+        s_m[wave][lane] = m_run;
+        s_l[wave][lane] = lw;
+    }
+    __syncthreads(); /* every wave is done with the Q^T operands */
+    f4_t *const mrg = (f4_t *)lds;
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; t++) mrg[(wave * 16u + t) * 64u + lane] = acc[t];
+    __syncthreads();
+    const bool fin = a.S == 1u;
+    float *pbase = fin ? nullptr : a.part + ((size_t)item * a.S + s) * gqa * PSTRIDE;
+    for (uint32_t e = tid; e < 16u * 256u; e += 256u) {
+        const uint32_t h = e >> 8, d = e & 255u;
+        if (h >= gqa) break; /* h grows with e */
+        /* dim d = 64 t + 4 (4 g + r) + u: tile 4 t + u, lane 16 g + h, row r */
+        const uint32_t t = d >> 6, g = (d >> 4) & 3u, r = (d >> 2) & 3u, u = d & 3u;
+        const uint32_t slot = (4u * t + u) * 64u + 16u * g + h;
+        float M = -INFINITY;
+#pragma unroll
+        for (uint32_t w = 0; w < 4u; w++) M = fmax2(M, s_m[w][h]);
+        float L = 0.f, x = 0.f;
+#pragma unroll
+        for (uint32_t w = 0; w < 4u; w++) {
+            const float mw = s_m[w][h];
+            const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+            L += f * s_l[w][h];
+            x += f * mrg[w * 16u * 64u + slot][r];
+        }
+        if (fin) {
+            float rv = L > 0.f ? x / L : 0.f;
+            if (it.gate) rv *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)h * 256u + d)));
+            stg(it.out + (size_t)h * 256u + d, rv);
+        } else {
+            stg(pbase + h * PSTRIDE + 2u + d, x);
+            if (d == 0u) stg((fv2 *)(pbase + h * PSTRIDE), (fv2){M, L});
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------
  * Prefill band kernel: the recent window that consecutive prefill tokens'
  * lists share, as dense MFMA tiles. A token's band is the longest run of
  * consecutive positions that ends its list (the causal recent window); the
@@ -2903,6 +3082,7 @@ struct Plan {
     uint32_t hg;  /* slab kernels: head groups of 8 */
     uint32_t S, cps;
     bool h16;     /* qsa_h16_k (f16 cache, hd 256) */
+    bool f32w;    /* qsa_f32w_k (f32 cache, hd 256) */
 };
 
 /* The slab kernel takes q8_0 / hd 256 shapes with 9 to 16 query heads per KV
@@ -2931,11 +3111,13 @@ static bool slab_takes(uint32_t gqa, bool prefill_sized) {
 template <int KIND, int MODE>
 static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t gqa,
                         bool have_part, size_t cap) {
-    Plan pl = {false, 1u, 1u, 1u, false};
-    if (KIND == Q4KV_F16 && hd == 256u && gqa <= 16u && h16_enabled()) {
+    Plan pl = {false, 1u, 1u, 1u, false, false};
+    const bool h16 = KIND == Q4KV_F16 && hd == 256u && gqa <= 16u && h16_enabled();
+    const bool f32w = KIND == Q4KV_F32 && hd == 256u && gqa <= 16u && f32w_enabled();
+    if (h16 || f32w) {
         /* one pass of every wave per split; prefill-sized launches stream
          * their passes through fewer splits */
-        const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 4u / hg * H16_SL;
+        const uint32_t hg = h16 && gqa > 8u ? 2u : 1u, ne = 4u / hg * 16u;
         const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
         uint32_t S = (uint64_t)n_items * s_full <= SLAB_MAX_WG ? s_full
                      : n_items >= SLAB_MAX_WG                  ? 1u
@@ -2945,7 +3127,8 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
         const size_t per = (size_t)gqa * PSTRIDE;
         while (S > 1u && (size_t)n_items * S * per > cap) S--;
         if (!have_part) S = 1u;
-        pl.h16 = true;
+        pl.h16 = h16;
+        pl.f32w = f32w;
         pl.hg = hg;
         pl.S = S;
         pl.cps = 0u;
@@ -2988,6 +3171,7 @@ static bool band_enabled(void) {
 /* A fused append + attention launch exists for this shape. */
 static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
     if (kind == Q4KV_F16) return hd == 256u && gqa <= 16u && h16_enabled();
+    if (kind == Q4KV_F32) return hd == 256u && gqa <= 16u && f32w_enabled();
     return kind == Q4KV_Q8 && hd == 256u && (gqa <= 8u || slab_takes(gqa, false));
 }
 
@@ -3004,7 +3188,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
     }
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
     const Plan pl = plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap);
-    if (IS_STEP(MODE) && !fast && !pl.slab && !pl.h16) return false; /* the fused append needs these */
+    if (IS_STEP(MODE) && !fast && !pl.slab && !pl.h16 && !pl.f32w) return false; /* the fused append needs these */
     const uint32_t S = pl.S, cps = pl.cps;
     a.S = S;
     a.cps = cps;
@@ -3036,7 +3220,9 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         /* double-buffered rows pay when a workgroup walks three or more chunks
          * (prefill, batched decode of many sequences); with one or two (the
          * 12-layer step) the extra LDS traffic does not */
-        if (pl.h16 && pl.hg == 1u)
+        if (pl.f32w)
+            qsa_f32w_k<MODE><<<grid, 256, 0, q4kv_stream>>>(a);
+        else if (pl.h16 && pl.hg == 1u)
             qsa_h16_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (pl.h16)
             qsa_h16_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
@@ -3187,6 +3373,8 @@ static bool step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32_t n
     const uint32_t gqa = n_head / n_kvh;
     if (step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F16)
         return launch_kind<Q4KV_F16, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, nullptr, pb);
+    if (step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F32)
+        return launch_kind<Q4KV_F32, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, nullptr, pb);
     if (step_fusable(kv_f16, hd, gqa))
         return launch_kind<Q4KV_Q8, MODE_STEP>(a, n_seq * n_kvh, max_n, gqa, nullptr, pb);
     /* other widths and shapes: the append launch, then the attention */
@@ -3258,6 +3446,8 @@ extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uin
             ? Plan{false, 1u, any_splits(n_items, max_n, gqa, have, q4kv_part_cap), 0u}
         : step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F16
             ? plan_launch<Q4KV_F16, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
+        : step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F32
+            ? plan_launch<Q4KV_F32, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
         : step_fusable(kv_f16, hd, gqa)
             ? plan_launch<Q4KV_Q8, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
         : kv_f16 == Q4KV_F32

@@ -124,7 +124,7 @@ def test_step_batch_q8_matches_append_then_decode(rt, oracle, n_seq):
     _check(rt, oracle, items, ctx, q4kv.KV_Q8, what=f"q8 {n_seq} layers")
 
 
-@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
 def test_step_batch_position_anywhere_in_list(rt, oracle, kind):
     """The new position listed first, in a middle chunk and twice, or not at
     all (then only the cache write shows it)."""
@@ -145,7 +145,7 @@ def test_step_batch_position_anywhere_in_list(rt, oracle, kind):
     _check(rt, oracle, items, ctx, kind, what=f"position anywhere, width {kind}")
 
 
-@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
 def test_step_batch_dense_items(rt, oracle, kind):
     """Dense items (no list): positions 0 .. pos, the new one last."""
     rng = np.random.default_rng(902 + kind)
@@ -156,15 +156,15 @@ def test_step_batch_dense_items(rt, oracle, kind):
 
 @pytest.mark.parametrize("kind", [q4kv.KV_F16, q4kv.KV_F32])
 def test_step_batch_other_widths(rt, oracle, kind):
-    """f16 caches take the fused launch (append inside the attention), f32
-    caches the append launch then the attention launch."""
+    """f16 and f32 caches: the fused launch (append inside the attention)
+    against the append launch then the attention launch."""
     rng = np.random.default_rng(903 + kind)
     ctx = 4096
     items, _ = _case(rng, oracle, 3, ctx, kind, lambda s: ctx - 1 - 300 * s, _sel_kv)
     _check(rt, oracle, items, ctx, kind, what=f"width {kind}")
 
 
-@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
 @pytest.mark.parametrize("n_head", [24, 32, 18])
 def test_step_batch_more_heads_per_kv_head(rt, oracle, n_head, kind):
     """The production layout (24 query heads over 2 KV heads, 12 per KV head),
@@ -177,7 +177,7 @@ def test_step_batch_more_heads_per_kv_head(rt, oracle, n_head, kind):
     _check(rt, oracle, items, ctx, kind, what=f"width {kind}, 12 layers, {n_head} heads")
 
 
-@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
 def test_step_batch_more_heads_position_anywhere(rt, oracle, kind):
     """24 heads: the new position first, in a middle split, twice, or not at all."""
     rng = np.random.default_rng(960 + kind)
