@@ -204,3 +204,45 @@ def test_any_shape_rejections(rt):
     assert not lib.q4_hip_qsa_decode_n(buf, buf, buf, buf, buf, 4, 1, 288, 1, 0, 8, 0.1, 1)
     assert not lib.q4_hip_qsa_decode_n(buf, buf, buf, buf, buf, 6, 4, 64, 1, 0, 8, 0.1, 1)
     rt.free(buf)
+
+
+@pytest.mark.parametrize("kind,n_head", [(1, 16), (1, 24), (0, 16), (0, 24)])
+def test_wide_prefill_multi_pass(rt, oracle, kind, n_head):
+    """f16 / f32 caches at hd 256 with enough items that each split streams
+    several passes per wave (the online softmax rescales across passes):
+    600 queries x 2 KV heads over 2051-entry lists, sampled rows against the
+    oracle, plus dense causal prefill over the same cache."""
+    note(f"wide prefill multi-pass kind={kind} n_head={n_head}")
+    rng = np.random.default_rng(1300 + kind + n_head)
+    n_kvh, hd, n_tok, base = 2, 256, 600, 3000
+    ctx = base + n_tok
+    k, v = heads(rng, (ctx, n_kvh)), heads(rng, (ctx, n_kvh))
+    q = heads(rng, (n_tok, n_head))
+    gate = rng.standard_normal((n_tok, n_head, hd)).astype(np.float32)
+    kc, _ = quantize_on_gpu(rt, k, kind)
+    vc, _ = quantize_on_gpu(rt, v, kind)
+    kb, vb = oracle.encode(k, kind), oracle.encode(v, kind)
+    width = 2051
+    sel = _lists(rng, n_tok, n_kvh, width, ctx, pad=0)
+    sel[::5, :, -100:] = -1  # some ragged lists
+    got = gpu_idx_kv(rt, q, kc, vc, kind, n_head, n_kvh, hd, sel.ravel(), width,
+                     n_kvh * width, width, ctx, gate=gate)
+    ts = np.unique(np.concatenate([[0, n_tok - 1], rng.choice(n_tok, 40, replace=False)]))
+    want = oracle.attn(q[ts], kb, vb, kind, n_head, n_kvh, hd, len(ts), gate=gate[ts],
+                       idx=sel[ts].ravel(), width=width, tok_stride=n_kvh * width,
+                       kvh_stride=width, max_kv=ctx, threads=8)
+    assert_attn_close(got[ts], want, what=f"wide prefill kind={kind} n_head={n_head}")
+    assert np.all(np.isfinite(got))
+    dq, dg = rt.upload(q), rt.upload(gate)
+    do = _out(rt, q.nbytes)
+    assert rt.lib.q4_hip_qsa_decode_n(dq, kc, vc, dg, do, n_head, n_kvh, hd, n_tok, base, ctx,
+                                      1.0 / 16, kind)
+    rt.sync()
+    got = rt.download(do, q.nbytes, np.float32).reshape(q.shape)
+    # dense causal rows: token t sees 0 .. base + t; check the sampled rows
+    for t in ts[:8]:
+        w1 = oracle.attn(q[t:t + 1], kb, vb, kind, n_head, n_kvh, hd, 1, gate=gate[t:t + 1],
+                         kv_base=base + int(t), max_kv=ctx)
+        assert_attn_close(got[t:t + 1], w1, what=f"dense prefill row {t}")
+    for p in (dq, dg, do, kc, vc):
+        rt.free(p)
