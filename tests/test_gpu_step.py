@@ -195,3 +195,78 @@ def test_step_batch_more_heads_position_anywhere(rt, oracle, kind):
         return base
     items, _ = _case(rng, oracle, 4, ctx, kind, lambda s: 5000 + 37 * s, sel_of, n_head=24)
     _check(rt, oracle, items, ctx, kind, what=f"24 heads, position anywhere, width {kind}")
+
+
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
+def test_step_batch_graph_replays(rt, oracle, kind):
+    """q4_hip_qsa_step_batch captured once into a graph and replayed four
+    times, each replay a new decode position with new rows, queries and
+    selections written between replays (descriptors included): every replay
+    matches the oracle over the cache as appended so far, and the caches end
+    byte-identical to the oracle's appends."""
+    note(f"graph-captured step_batch kind={kind}")
+    rng = np.random.default_rng(970 + kind)
+    n_seq, ctx, base = 3, 6000, 5000
+    bpt = q4kv.token_bytes(kind, N_KVH, HD)
+    lib = rt.lib
+    hk, hv, kcs, vcs = [], [], [], []
+    for s in range(n_seq):
+        k, v = heads(rng, (ctx, N_KVH)), heads(rng, (ctx, N_KVH))
+        k[base:] = 0.0
+        v[base:] = 0.0
+        hk.append(oracle.encode(k, kind).copy())
+        hv.append(oracle.encode(v, kind).copy())
+        kcs.append(rt.upload(hk[-1]))
+        vcs.append(rt.upload(hv[-1]))
+    dq = [rt.alloc(N_HEAD * HD * 4) for _ in range(n_seq)]
+    dkn = [rt.alloc(N_KVH * HD * 4) for _ in range(n_seq)]
+    dvn = [rt.alloc(N_KVH * HD * 4) for _ in range(n_seq)]
+    dsel = [rt.alloc(N_KVH * WIDTH * 4) for _ in range(n_seq)]
+    dout = [rt.alloc(N_HEAD * HD * 4) for _ in range(n_seq)]
+    dd = rt.alloc(ctypes.sizeof(q4kv.StepDesc) * n_seq)
+
+    def descs(pos):
+        steps = (q4kv.StepDesc * n_seq)()
+        for s in range(n_seq):
+            seq = q4kv.SeqDesc(kcs[s], vcs[s], dq[s], None, dout[s], dsel[s], WIDTH, WIDTH,
+                               ctx, 0)
+            steps[s] = q4kv.StepDesc(seq, dkn[s], dvn[s], pos)
+        assert lib.q4_hip_h2d(dd, ctypes.addressof(steps), ctypes.sizeof(steps))
+        rt.sync()
+
+    descs(base)
+    assert lib.q4_hip_graph_begin() == 1
+    ok = lib.q4_hip_qsa_step_batch(dd, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, kind, WIDTH)
+    g = lib.q4_hip_graph_end()
+    assert ok and g
+    try:
+        for pos in (base, base + 1, base + 2, base + 3):
+            qs, sels = [], []
+            for s in range(n_seq):
+                q = heads(rng, (1, N_HEAD))
+                kn, vn = heads(rng, (N_KVH,)), heads(rng, (N_KVH,))
+                sel = np.stack([selection(rng, pos) for _ in range(N_KVH)])
+                rt.h2d(dq[s], q)
+                rt.h2d(dkn[s], kn)
+                rt.h2d(dvn[s], vn)
+                rt.h2d(dsel[s], sel)
+                hk[s][pos * bpt:(pos + 1) * bpt] = oracle.encode(kn, kind)
+                hv[s][pos * bpt:(pos + 1) * bpt] = oracle.encode(vn, kind)
+                qs.append(q)
+                sels.append(sel)
+            descs(pos)
+            assert lib.q4_hip_graph_launch(g)
+            rt.sync()
+            for s in range(n_seq):
+                got = rt.download(dout[s], qs[s].nbytes, np.float32).reshape(qs[s].shape)
+                want = oracle.attn(qs[s], hk[s], hv[s], kind, N_HEAD, N_KVH, HD, 1,
+                                   idx=sels[s].ravel(), width=WIDTH, tok_stride=N_KVH * WIDTH,
+                                   kvh_stride=WIDTH, max_kv=ctx, scale=1.0 / 16)
+                assert_attn_close(got, want, what=f"replay pos {pos} seq {s}")
+        for s in range(n_seq):
+            assert np.array_equal(rt.download(kcs[s], hk[s].size), hk[s])
+            assert np.array_equal(rt.download(vcs[s], hv[s].size), hv[s])
+    finally:
+        lib.q4_hip_graph_free(g)
+        for p in kcs + vcs + dq + dkn + dvn + dsel + dout + [dd]:
+            rt.free(p)
