@@ -65,7 +65,10 @@ bool q4_hip_f32_to_f16(void *dst_f16, const float *src, uint64_t n);
 bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k, const float *v,
                         uint32_t n, uint32_t bpt, int kind);
 
-/* ---------------- QSA attention (a5-a9) ---------------- */
+/* ---------------- QSA attention (a5-a9) ----------------
+ * Shapes, as the reference accepts them: head_dim 1..256 (a multiple of 32
+ * for q8_0, whose rows are 32-element blocks), n_head a multiple of n_kvh,
+ * any number of query heads per KV head. */
 /* Dense causal attention: token t of n_tok attends positions
  * 0 .. min(kv_base+t+1, max_kv)-1. q/gate/out are [n_tok][n_head][hd] fp32;
  * out = softmax(q.k*scale) @ v * sigmoid(gate) (src/q4.h:906-909). */
@@ -173,8 +176,10 @@ bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n_seq,
 
 /* One decode step of one item: append the token's K and V rows at pos, then
  * attend -- q4_hip_kv_append_batch followed by q4_hip_qsa_decode_batch, in
- * one launch when the cache is q8_0 with head_dim 256. The attention sees
- * the new row wherever its position list names pos. 96 bytes, device memory. */
+ * one launch when head_dim is 256 with at most 16 query heads per KV head
+ * (any width; otherwise an append launch precedes the attention). The
+ * attention sees the new row wherever its position list names pos. 96 bytes,
+ * device memory. */
 typedef struct {
     q4kv_seq_desc seq;      /* caches, query, gate, output, position lists */
     const float *k, *v;     /* the token's rows, [n_kvh][hd] fp32 each */

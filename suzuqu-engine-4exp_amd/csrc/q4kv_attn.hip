@@ -3110,10 +3110,13 @@ static bool slab_takes(uint32_t gqa, bool prefill_sized) {
 
 template <int KIND, int MODE>
 static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t gqa,
-                        bool have_part, size_t cap) {
+                        bool have_part, size_t cap, bool rows16 = true) {
+    /* rows16: the caches are 16-byte aligned (the slab, f16 and f32 kernels
+     * fetch 16-byte pieces; the chunk and generic kernels check for
+     * themselves) */
     Plan pl = {false, 1u, 1u, 1u, false, false};
-    const bool h16 = KIND == Q4KV_F16 && hd == 256u && gqa <= 16u && h16_enabled();
-    const bool f32w = KIND == Q4KV_F32 && hd == 256u && gqa <= 16u && f32w_enabled();
+    const bool h16 = KIND == Q4KV_F16 && hd == 256u && gqa <= 16u && rows16 && h16_enabled();
+    const bool f32w = KIND == Q4KV_F32 && hd == 256u && gqa <= 16u && rows16 && f32w_enabled();
     if (h16 || f32w) {
         /* one pass of every wave per split; prefill-sized launches stream
          * their passes through fewer splits */
@@ -3137,7 +3140,7 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
     const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
     const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
     const bool prefill_sized = (uint64_t)n_items * s_full > SLAB_MAX_WG;
-    if (KIND == Q4KV_Q8 && hd == 256u && slab_takes(gqa, prefill_sized)) {
+    if (KIND == Q4KV_Q8 && hd == 256u && rows16 && slab_takes(gqa, prefill_sized)) {
         /* many items (prefill): fewer splits, each wave streaming its passes */
         uint32_t S = !prefill_sized ? s_full : n_items >= SLAB_MAX_WG ? 1u : SLAB_MAX_WG / n_items;
         if (S < 1u) S = 1u;
@@ -3187,7 +3190,11 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         }
     }
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
-    const Plan pl = plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap);
+    /* batch modes: the caches are in device descriptors, 16-byte aligned by
+     * contract */
+    const bool rows16 = IS_BATCH(MODE) || ((((uintptr_t)a.kc) | ((uintptr_t)a.vc)) & 15u) == 0u;
+    const Plan pl =
+        plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap, rows16);
     if (IS_STEP(MODE) && !fast && !pl.slab && !pl.h16 && !pl.f32w) return false; /* the fused append needs these */
     const uint32_t S = pl.S, cps = pl.cps;
     a.S = S;

@@ -246,3 +246,32 @@ def test_wide_prefill_multi_pass(rt, oracle, kind, n_head):
         assert_attn_close(got[t:t + 1], w1, what=f"dense prefill row {t}")
     for p in (dq, dg, do, kc, vc):
         rt.free(p)
+
+
+@pytest.mark.parametrize("kind,n_head,n_tok,off", [(2, 16, 2, 2), (2, 24, 2, 2), (1, 16, 2, 2),
+                                                  (1, 24, 2, 2), (0, 16, 2, 4), (2, 16, 600, 2)])
+def test_unaligned_caches(rt, oracle, kind, n_head, n_tok, off):
+    """Caches that are not 16-byte aligned (base + off bytes) take kernels that
+    read them in smaller pieces; results as for aligned caches. The 600-token
+    q8_0 case is prefill-sized (otherwise the band and slab kernels)."""
+    note(f"unaligned caches kind={kind} n_head={n_head} n_tok={n_tok} off={off}")
+    rng = np.random.default_rng(1400 + kind + n_head + n_tok)
+    n_kvh, hd, ctx, width = 2, 256, 5000, 2051
+    k, v = heads(rng, (ctx, n_kvh)), heads(rng, (ctx, n_kvh))
+    q = heads(rng, (n_tok, n_head))
+    gate = rng.standard_normal((n_tok, n_head, hd)).astype(np.float32)
+    kb, vb = oracle.encode(k, kind), oracle.encode(v, kind)
+    kbuf, vbuf = rt.alloc(kb.nbytes + 64), rt.alloc(vb.nbytes + 64)
+    rt.h2d(kbuf + off, kb)
+    rt.h2d(vbuf + off, vb)
+    sel = _lists(rng, n_tok, n_kvh, width, ctx, pad=20)
+    got = gpu_idx_kv(rt, q, kbuf + off, vbuf + off, kind, n_head, n_kvh, hd, sel.ravel(),
+                     width, n_kvh * width, width, ctx, gate=gate)
+    ts = np.arange(n_tok) if n_tok <= 8 else np.unique(
+        np.concatenate([[0, n_tok - 1], rng.choice(n_tok, 30, replace=False)]))
+    want = oracle.attn(q[ts], kb, vb, kind, n_head, n_kvh, hd, len(ts), gate=gate[ts],
+                       idx=sel[ts].ravel(), width=width, tok_stride=n_kvh * width,
+                       kvh_stride=width, max_kv=ctx, threads=8)
+    assert_attn_close(got[ts], want, what=f"unaligned kind={kind} n_head={n_head}")
+    rt.free(kbuf)
+    rt.free(vbuf)
