@@ -268,15 +268,29 @@ __device__ uint64_t q4kv_trace_buf[4096 * 16];
             q4kv_trace_buf[((blockIdx.y * gridDim.x + blockIdx.x) & 4095u) * 16u + (slot)] = \
                 wall_clock64();                                                    \
     } while (0)
+/* per wave: [wave][slot] for the first 4096 waves of the launch (later
+ * waves are not recorded, so no slot mixes two waves) */
 #define TRACEW(slot)                                                                   \
     do {                                                                               \
-        if ((threadIdx.x & 63u) == 0)                                                  \
-            q4kv_trace_buf[((((blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x >> 6)) + (threadIdx.x >> 6)) & \
-                            4095u) * 16u + (slot)] = wall_clock64();                   \
+        const uint32_t tw_ = (blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x >> 6) + \
+                             (threadIdx.x >> 6);                                       \
+        if ((threadIdx.x & 63u) == 0 && tw_ < 4096u)                                   \
+            q4kv_trace_buf[tw_ * 16u + (slot)] = wall_clock64();                       \
+    } while (0)
+/* the prefill band kernel's own per-wave stamps (it runs before the slab
+ * kernel of the same call, which would overwrite q4kv_trace_buf) */
+__device__ uint64_t q4kv_trace_band[4096 * 16];
+#define TRACEB(slot)                                                                   \
+    do {                                                                               \
+        const uint32_t tw_ = (blockIdx.y * gridDim.x + blockIdx.x) * (blockDim.x >> 6) + \
+                             (threadIdx.x >> 6);                                       \
+        if ((threadIdx.x & 63u) == 0 && tw_ < 4096u)                                   \
+            q4kv_trace_band[tw_ * 16u + (slot)] = wall_clock64();                      \
     } while (0)
 #else
 #define TRACE(slot) do { } while (0)
 #define TRACEW(slot) do { } while (0)
+#define TRACEB(slot) do { } while (0)
 #endif
 
 template <int KIND> struct KCfg;
@@ -2312,11 +2326,55 @@ __device__ static inline uint32_t band_of(const int32_t *list, uint32_t width, u
         }
         run = w0 + 64u;
     }
+    /* a run stops at position 0 (a -1 entry before it equals vend - run too) */
+    if ((int64_t)run > (int64_t)vend + 1) run = (uint32_t)vend + 1u;
     if (run > BAND_SPAN) run = BAND_SPAN;
     if (run < BAND_MIN) return width;
     ps = vend - (int32_t)run + 1;
     pe = vend;
     return (uint32_t)(e - (int32_t)run + 1);
+}
+
+/* band_of with every load issued at once: the last BAND_NJ x 64 entries of
+ * the list (one load per lane each) cover the run whenever the list's last
+ * valid entry is among its final 64 (no more than 63 trailing padding or
+ * out-of-range entries); otherwise the chained band_of runs. Same result. */
+constexpr uint32_t BAND_NJ = BAND_SPAN / 64u + 1u;
+__device__ static inline uint32_t band_of_tail(const int32_t *list, uint32_t width,
+                                               uint32_t max_kv, uint32_t lane, int32_t &ps,
+                                               int32_t &pe) {
+    int32_t v[BAND_NJ];
+#pragma unroll
+    for (uint32_t i = 0; i < BAND_NJ; i++) {
+        const uint32_t j = 64u * i + lane; /* entry width - 1 - j */
+        v[i] = j < width ? ldg(list + (width - 1u - j)) : -1;
+    }
+    /* the last valid entry: the smallest j with a valid position */
+    const uint64_t okb = __ballot(v[0] >= 0 && (uint32_t)v[0] < max_kv);
+    if (!okb) return band_of(list, width, max_kv, lane, ps, pe);
+    const uint32_t jf = (uint32_t)__builtin_ctzll(okb);
+    const int32_t vend = __shfl(v[0], (int)jf);
+    /* the run: entry width - 1 - j holds vend - (j - jf) for j = jf, jf + 1, .. */
+    uint32_t run = BAND_NJ * 64u - jf; /* every loaded entry from jf on matches */
+#pragma unroll
+    for (uint32_t i = 0; i < BAND_NJ; i++) {
+        const uint32_t j = 64u * i + lane;
+        const bool bad = j >= jf && (j >= width || v[i] != vend - (int32_t)(j - jf));
+        const uint64_t bb = __ballot(bad);
+        if (bb) {
+            run = min(run, 64u * i + (uint32_t)__builtin_ctzll(bb) - jf);
+            break;
+        }
+    }
+    ps = 1;
+    pe = 0;
+    /* a run stops at position 0 (a -1 entry before it equals vend - run too) */
+    if ((int64_t)run > (int64_t)vend + 1) run = (uint32_t)vend + 1u;
+    if (run > BAND_SPAN) run = BAND_SPAN;
+    if (run < BAND_MIN) return width;
+    ps = vend - (int32_t)run + 1;
+    pe = vend;
+    return width - 1u - jf - run + 1u;
 }
 
 __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
@@ -2342,7 +2400,7 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
     const size_t rstride = (size_t)a.n_kvh * ROWB;
     const uint8_t *kbase = a.kc + (size_t)kh * ROWB, *vbase = a.vc + (size_t)kh * ROWB;
 
-    TRACEW(0);
+    TRACEB(0);
     /* ---- the bands of this wave's tokens ---- */
     int32_t ps[TW], pe[TW];
     uint32_t nb[TW];
@@ -2353,8 +2411,8 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
         pe[k] = 0;
         nb[k] = width;
         if (t < n_tok)
-            nb[k] = band_of(a.idx + (size_t)t * a.tok_stride + (size_t)kh * a.kvh_stride, width,
-                            a.max_kv, lane, ps[k], pe[k]);
+            nb[k] = band_of_tail(a.idx + (size_t)t * a.tok_stride + (size_t)kh * a.kvh_stride,
+                                 width, a.max_kv, lane, ps[k], pe[k]);
         if (lane == 0) {
             s_ps[wave * TW + k] = ps[k];
             s_pe[wave * TW + k] = pe[k];
@@ -2385,7 +2443,7 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
         }
     }
     if (!tile) return; /* uniform over the workgroup */
-    TRACEW(1);
+    TRACEB(1);
     const uint32_t n_pass = (uint32_t)(hi - lo) / BP + 1u;
 
     /* the Q^T operands of this wave's tokens, natural dim order */
@@ -2433,7 +2491,7 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
     for (uint32_t k = 0; k < TW; k++)
 #pragma unroll
         for (uint32_t bb = 0; bb < 8u; bb++) asm volatile("" ::"v"(qB[k][bb]));
-    TRACEW(2);
+    TRACEB(2);
     issue(0u, rawA);
     if (n_pass > 1u) issue(1u, rawB);
 
@@ -2460,7 +2518,7 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
             __builtin_amdgcn_s_waitcnt(0);
         }
         barrier_lds(); /* rows landed; every wave done with the last pass */
-        if (pass == 4u) TRACEW(3);
+        if (pass == 4u) TRACEB(3);
         /* ---- dequantise: K' rows (work item: position x >> 4, 16 dims) ---- */
 #pragma unroll
         for (uint32_t x = tid; x < 512u; x += 64u * BAND_WAVES) {
@@ -2511,7 +2569,7 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
             *(u4_t *)&vt[1][2u * dp + 1u][8u * g] = (u4_t){lo4[0], lo4[1], lo4[2], lo4[3]};
         }
         barrier_lds(); /* K', V'^T ready; this pass's raw rows are free */
-        if (pass == 4u) TRACEW(4);
+        if (pass == 4u) TRACEB(4);
         if (pass + 2u < n_pass) issue(pass + 2u, rawb);
         const int32_t base = lo + (int32_t)(pass * BP);
         bool live[TW], any = false;
@@ -2521,7 +2579,7 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
             any = any || live[k];
         }
         if (!any) return; /* wave-uniform */
-        if (pass == 4u) TRACEW(5);
+        if (pass == 4u) TRACEB(5);
         /* ---- scores of the tokens' 8 heads at the pass's 32 positions ---- */
         f4_t S[TW][2];
 #pragma unroll
@@ -2581,13 +2639,14 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
                     acc[k][T2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[k], acc[k][T2], 0, 0, 0);
             }
         }
+        TRACEB(8u + (pass < 7u ? pass : 7u));
     };
     for (uint32_t pass = 0; pass < n_pass; pass += 2u) {
         run_pass(pass, rawA);
-        if (pass == 4u) TRACEW(6);
+        if (pass == 4u) TRACEB(6);
         if (pass + 1u < n_pass) run_pass(pass + 1u, rawB);
     }
-    TRACEW(7);
+    TRACEB(7);
     /* ---- the partials: (m, l) per head, unnormalised rows in out ---- */
 #pragma unroll
     for (uint32_t k = 0; k < TW; k++) {
@@ -3478,6 +3537,11 @@ extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uin
 extern "C" int q4kv_trace_read(uint64_t *host, size_t n) {
     if (hipDeviceSynchronize() != hipSuccess) return -1;
     return hipMemcpyFromSymbol(host, HIP_SYMBOL(q4kv_trace_buf), n * sizeof(uint64_t), 0,
+                               hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+extern "C" int q4kv_trace_read_band(uint64_t *host, size_t n) {
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(q4kv_trace_band), n * sizeof(uint64_t), 0,
                                hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
 }
 #endif

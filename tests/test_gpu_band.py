@@ -11,6 +11,7 @@ oracle (|got - ref| <= 2e-3 + 1e-3*|ref|):
 - runs ending far from their neighbours' (a token group whose runs span
   more than 1024 positions falls back to the general kernel);
 - runs longer than 1024 positions (the band takes their last 1024);
+- right-aligned lists (-1 padding first, then a run from position 0);
 - a token count that is not a multiple of the 16-token band tile;
 - 8, 4 and 1 query heads per KV head, with and without the gate.
 
@@ -69,6 +70,12 @@ def band_lists(rng, n_tok, n_kvh, width, base, ctx, long_run):
                 sel = np.concatenate([_prefix(rng, 0, e - 81, width - 80),
                                       np.arange(e - 79, e + 1)])
             out[t, kh, : sel.size] = sel
+            if (t // 16) % 5 == 4:
+                # right-aligned: -1 padding first, then positions 0 .. L - 1
+                # (a -1 right before a run down to position 0 must not extend it)
+                L = 100 + t % 16
+                out[t, kh, :] = -1
+                out[t, kh, width - L:] = np.arange(L)
     return out
 
 
@@ -97,7 +104,7 @@ def test_prefill_band_split(rt, oracle, n_head, width, gated, long_run):
     kb, vb = oracle.quant_q8(k), oracle.quant_q8(v)
     # three whole 16-token groups (one of them holding a far run), the ragged
     # last group and a random sample
-    ts = np.unique(np.concatenate([np.arange(0, 16), np.arange(48, 64), np.arange(160, 176),
+    ts = np.unique(np.concatenate([np.arange(0, 16), np.arange(48, 80), np.arange(160, 176),
                                    np.arange(N_TOK - 8, N_TOK),
                                    rng.choice(N_TOK, 200, replace=False)]))
     want = oracle.attn(q[ts], kb, vb, 2, n_head, n_kvh, hd, len(ts),
