@@ -61,7 +61,7 @@ def _step(rt, items, ctx, kind, entry):
     return res
 
 
-@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16])
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
 def test_noalloc_step_matches_step_batch_twice(rt, oracle, kind):
     ctx = 8192
     for call, n_seq in enumerate((12, 3)):
