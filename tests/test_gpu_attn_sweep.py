@@ -45,7 +45,7 @@ def _list(rng, width, ctx, end):
     """One list of `width` entries in one of several shapes."""
     shape = rng.integers(0, 7)
     if shape == 0:      # sorted distinct, trailing padding
-        n = int(rng.integers(0, width + 1))
+        n = int(rng.integers(0, min(width, ctx) + 1))
         sel = np.sort(rng.choice(ctx, n, replace=False))
         out = np.full(width, -1, np.int64)
         out[:n] = sel
