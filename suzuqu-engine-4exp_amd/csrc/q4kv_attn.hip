@@ -1252,10 +1252,10 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
  *    the exponent trick: 1152 + k), B = Q^T for 16 columns: columns 0-7 the
  *    fp16 part (truncated) of 8 query heads' q, pre-scaled to log2 units,
  *    columns 8-15 the fp16 residual, so a score is column c plus column c + 8.
- *  - The +1152 bias and the per-position q8_0 scales: S = sum_b ks[p][b] C_b
- *    + C', where one more MFMA gives C'[p][c] = sum_b ks[p][b] qbias[b][c]
- *    with qbias = -1152 sum_k q split into three fp16 parts (K slots 0-23),
- *    and slot 24 carries -65504 for list entries that are padding.
+ *  - The K operands lose the +1152 bias in four packed fp16 subtracts (exact:
+ *    k is an integer), so the per-block products sum at the size of q.k for
+ *    any |q|; the per-position q8_0 scales: S = sum_b ks[p][b] C_b, started
+ *    at -inf for list entries that are padding.
  *  - A lane's C rows (4 positions of each 16-position tile) are exactly the
  *    8 K slots its P.V B operand needs, so the softmax weights never leave
  *    the lane: P.V runs as O^T = V^T.P^T with B = the weights times the V
@@ -1333,13 +1333,11 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     constexpr uint32_t RBYTES = 2u * NE * ROWB;           /* K rows | V rows */
     constexpr uint32_t MBYTES = 4u * 16u * 8u * 20u * 4u;  /* merge: [wave][tile][head][20] */
     __shared__ __attribute__((aligned(16))) uint8_t rows[RBYTES > MBYTES ? RBYTES : MBYTES];
-    /* Q^T operands [head group][block][k-group][column][8 fp16] and the bias
-     * operand [head group][k-group][column][8 fp16] */
+    /* Q^T operands [head group][block][k-group][column][8 fp16] */
     __shared__ __attribute__((aligned(16))) uint16_t qB[HG][8][4][16][8];
-    __shared__ __attribute__((aligned(16))) uint16_t qbB[HG][4][16][8];
     /* V block scales of each slab, block-major (fp16 bits, 0 at padding) */
     __shared__ __attribute__((aligned(16))) uint16_t vsT[NSLAB][8][SLAB];
-    __shared__ int32_t s_pos[NE];
+    __shared__ __attribute__((aligned(16))) int32_t s_pos[NE];
     __shared__ float s_m[4][8], s_l[4][8];
     /* MODE_PSTEP: the prepared query rows and the prepared new key row */
     constexpr bool PREP = MODE == MODE_PSTEP;
@@ -1484,41 +1482,17 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         }
     }
 
-    /* ---- Q^T operands and the bias operand, built once per workgroup ---- */
+    /* ---- Q^T operands, built once per workgroup ---- */
 #pragma unroll
     for (uint32_t k = 0; k < HG; k++) {
         uint32_t hw[4], lw[4];
-        float sh = 0.f, sl = 0.f;
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
             hw[i] = pkrtz(qx[k][2u * i], qx[k][2u * i + 1u]);
             lw[i] = pkrtz(qx[k][2u * i] - h2lo(hw[i]), qx[k][2u * i + 1u] - h2hi(hw[i]));
-            sh += h2lo(hw[i]) + h2hi(hw[i]);
-            sl += h2lo(lw[i]) + h2hi(lw[i]);
         }
         *(u4_t *)&qB[k][t_b][t_kg][t_hh][0] = (u4_t){hw[0], hw[1], hw[2], hw[3]};
         *(u4_t *)&qB[k][t_b][t_kg][t_hh + 8u][0] = (u4_t){lw[0], lw[1], lw[2], lw[3]};
-        /* the block's column sums: the four k-groups are a lane quad */
-        sh += dppf<0xB1>(sh);
-        sh += dppf<0x4E>(sh);
-        sl += dppf<0xB1>(sl);
-        sl += dppf<0x4E>(sl);
-        if (t_kg == 0u) {
-#pragma unroll
-            for (uint32_t lo = 0; lo < 2u; lo++) {
-                const float x = -1152.f * (lo ? sl : sh);
-                const _Float16 p1 = (_Float16)x;
-                const float r1 = x - (float)p1;
-                const _Float16 p2 = (_Float16)r1;
-                const _Float16 p3 = (_Float16)(r1 - (float)p2);
-                const uint32_t col = t_hh + 8u * lo;
-                qbB[k][0][col][t_b] = __builtin_bit_cast(uint16_t, p1);
-                qbB[k][1][col][t_b] = __builtin_bit_cast(uint16_t, p2);
-                qbB[k][2][col][t_b] = __builtin_bit_cast(uint16_t, p3);
-            }
-        }
-        if (tid < 16u) /* slot 24: the padding penalty (fp16 -65504) */
-            *(u4_t *)&qbB[k][3][tid][0] = (u4_t){0xFBFFu, 0u, 0u, 0u};
     }
     __syncthreads();
     TRACEW(2);
@@ -1529,7 +1503,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     for (uint32_t t = 0; t < 16u; t++) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
     const h8_t neg = (h8_t)((_Float16)-1152.0f);
     const uint16_t *const qBw = &qB[hg][0][jg][c][0];
-    const h8_t qbias_op = *(const h8_t *)&qbB[hg][jg][c][0];
+    const h8_t k_bias = (h8_t)((_Float16)1152.0f);
 
     for (uint32_t pass = 0; pass < n_pass; pass++) {
         if (pass > 0u) any = issue(pass, ne, pos);
@@ -1582,26 +1556,24 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             f4_t S[2];
 #pragma unroll
             for (uint32_t t = 0; t < 2u; t++) {
-                /* A' row p = 16 t + c: the 8 K scales (k-groups 0-2), or the
-                 * padding flag (k-group 3) */
-                const uint8_t *rp = krow + (16u * t + c) * ROWB;
-                u4_t w;
-#pragma unroll
-                for (uint32_t i = 0; i < 4u; i++) w[i] = lds_u16x2(rp + 68u * i, rp + 68u * i + 34u);
-                const bool pad = s_pos[slab * SLAB + 16u * t + c] < 0;
-                const u4_t wf = {pad ? 0x3C00u : 0u, 0u, 0u, 0u};
-                const u4_t ap = jg == 3u ? wf : w;
-                S[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, ap),
-                                                              qbias_op,
-                                                              (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                /* this lane's rows 4 jg .. 4 jg + 3 of tile t: padding rows
+                 * start at -inf (their K scales are zero and their bytes
+                 * finite, so they stay there; a pass that is computed holds a
+                 * valid row, so the maximum is finite) */
+                const int4 ps = *(const int4 *)&s_pos[slab * SLAB + 16u * t + 4u * jg];
+                S[t] = (f4_t){ps.x < 0 ? -INFINITY : 0.f, ps.y < 0 ? -INFINITY : 0.f,
+                              ps.z < 0 ? -INFINITY : 0.f, ps.w < 0 ? -INFINITY : 0.f};
             }
 #pragma unroll
             for (uint32_t b = 0; b < 8u; b++) {
                 const h8_t qb = *(const h8_t *)(qBw + b * 4u * 16u * 8u);
 #pragma unroll
                 for (uint32_t t = 0; t < 2u; t++) {
+                    /* exact k: the products need no bias correction, so their
+                     * sum rounds at the size of q.k whatever |q| */
                     const h8_t kb =
-                        k_operand_biased(krow + (16u * t + c) * ROWB, b, jg, k_eoff, k_esel);
+                        k_operand_biased(krow + (16u * t + c) * ROWB, b, jg, k_eoff, k_esel) -
+                        k_bias;
                     const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                         kb, qb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     const uint8_t *rs = krow + (16u * t + 4u * jg) * ROWB + 34u * b;

@@ -1,0 +1,57 @@
+"""Query rows of large magnitude on the head_dim-256 q8_0 kernels (chunk,
+slab, band), against the oracle (|got - ref| <= 2e-3 + 1e-3*|ref|).
+
+The kernels carry Q as fp16 hi/lo parts, so |q| (times the softmax scale
+where a kernel folds it in) must stay inside fp16's range; within that
+range the results must not depend on the magnitude. The slab kernel also
+folds the +1152 bias of its int8 -> fp16 K operands into one MFMA whose
+operand is -1152 x (the sum of a 32-dimension block of q x scale), split
+into fp16 parts: here one block of every head sums to +704 and another to
+-640 (about +63 and -58 after the scale, so -1152 x that is beyond fp16's
+65504), which that operand must still represent.
+
+Within fp16's range the results must not depend on the magnitude: the
+slab kernel's K operands are exact (no bias left in the products); the chunk
+kernel removes the bias through the accumulator input of each block's
+MFMA."""
+import numpy as np
+import pytest
+
+from gpu_util import note, quantize_on_gpu
+from synth import assert_attn_close, heads, selection
+from test_gpu_attn import gpu_idx_kv
+
+pytestmark = pytest.mark.gpu
+
+
+# (query heads, tokens): decode through the chunk kernel (8 per KV head) and
+# the slab kernel (16); prefill-sized launches through the band + slab
+# kernels (8 and 16 per KV head)
+@pytest.mark.parametrize("n_head,n_tok", [(16, 1), (32, 1), (16, 700), (32, 300)])
+def test_large_query_blocks(rt, oracle, n_head, n_tok):
+    n_kvh, hd, width = 2, 256, 2051
+    note(f"large query blocks n_head={n_head} n_tok={n_tok}")
+    rng = np.random.default_rng(9100 + n_head + n_tok)
+    base = 6000
+    ctx = base + n_tok
+    k, v = heads(rng, (ctx, n_kvh)), heads(rng, (ctx, n_kvh))
+    q = heads(rng, (n_tok, n_head))
+    # block 0 sums to about +704, block 3 to about -640 (not exactly
+    # representable sums, as real queries give)
+    q[:, :, 0:32] = 22.0 + 3.0 * rng.standard_normal((n_tok, n_head, 32), dtype=np.float32)
+    q[:, :, 96:128] = -20.0 + 3.0 * rng.standard_normal((n_tok, n_head, 32), dtype=np.float32)
+    kc, _ = quantize_on_gpu(rt, k, 2)
+    vc, _ = quantize_on_gpu(rt, v, 2)
+    sel = np.stack([np.stack([selection(rng, base + t) for _ in range(n_kvh)])
+                    for t in range(n_tok)]).astype(np.int32)
+    got = gpu_idx_kv(rt, q, kc, vc, 2, n_head, n_kvh, hd, sel.ravel(), width, n_kvh * width,
+                     width, ctx)
+    rt.free(kc)
+    rt.free(vc)
+    kb, vb = oracle.quant_q8(k), oracle.quant_q8(v)
+    ts = np.arange(n_tok) if n_tok <= 8 else np.unique(
+        np.concatenate([[0, n_tok - 1], rng.choice(n_tok, 40, replace=False)]))
+    want = oracle.attn(q[ts], kb, vb, 2, n_head, n_kvh, hd, len(ts), idx=sel[ts].ravel(),
+                       width=width, tok_stride=n_kvh * width, kvh_stride=width, max_kv=ctx,
+                       threads=8)
+    assert_attn_close(got[ts], want, what=f"large query blocks n_head={n_head} n_tok={n_tok}")
