@@ -1,4 +1,4 @@
-"""Query rows of large magnitude on the head_dim-256 q8_0 kernels (chunk,
+"""Values of large magnitude on the head_dim-256 q8_0 kernels (chunk,
 slab, band), against the oracle (|got - ref| <= 2e-3 + 1e-3*|ref|).
 
 The kernels carry Q as fp16 hi/lo parts, so |q| (times the softmax scale
@@ -55,3 +55,37 @@ def test_large_query_blocks(rt, oracle, n_head, n_tok):
                        width=width, tok_stride=n_kvh * width, kvh_stride=width, max_kv=ctx,
                        threads=8)
     assert_attn_close(got[ts], want, what=f"large query blocks n_head={n_head} n_tok={n_tok}")
+
+
+@pytest.mark.parametrize("n_head,n_tok", [(16, 1), (32, 1), (16, 700), (32, 300)])
+def test_large_v_values(rt, oracle, n_head, n_tok):
+    """V values up to ~2.4e4 (block scales up to ~190; the band kernel's fp16
+    parts of v * scale stay below 65504), K and Q at unit scale. The outputs
+    are the unit-scale outputs times 1000, so the bar is the unit-scale bar
+    times 1000: |got - ref| <= 2 + 1e-3*|ref|. (The chunk and slab kernels
+    carry V as 1152 + v and remove the bias on the MFMA pipe, so their error
+    is ~1e-5 of a V block's absmax: ~5e-4 at unit scale, ~0.25 here.)"""
+    n_kvh, hd, width = 2, 256, 2051
+    note(f"large v values n_head={n_head} n_tok={n_tok}")
+    rng = np.random.default_rng(9300 + n_head + n_tok)
+    base = 6000
+    ctx = base + n_tok
+    k = heads(rng, (ctx, n_kvh))
+    v = heads(rng, (ctx, n_kvh)) * np.float32(1000.0)
+    q = heads(rng, (n_tok, n_head))
+    kc, _ = quantize_on_gpu(rt, k, 2)
+    vc, _ = quantize_on_gpu(rt, v, 2)
+    sel = np.stack([np.stack([selection(rng, base + t) for _ in range(n_kvh)])
+                    for t in range(n_tok)]).astype(np.int32)
+    got = gpu_idx_kv(rt, q, kc, vc, 2, n_head, n_kvh, hd, sel.ravel(), width, n_kvh * width,
+                     width, ctx)
+    rt.free(kc)
+    rt.free(vc)
+    kb, vb = oracle.quant_q8(k), oracle.quant_q8(v)
+    ts = np.arange(n_tok) if n_tok <= 8 else np.unique(
+        np.concatenate([[0, n_tok - 1], rng.choice(n_tok, 40, replace=False)]))
+    want = oracle.attn(q[ts], kb, vb, 2, n_head, n_kvh, hd, len(ts), idx=sel[ts].ravel(),
+                       width=width, tok_stride=n_kvh * width, kvh_stride=width, max_kv=ctx,
+                       threads=8)
+    assert_attn_close(got[ts], want, atol=2.0, rtol=1e-3,
+                      what=f"large v values n_head={n_head} n_tok={n_tok}")
