@@ -4,8 +4,9 @@ bytes per token, positions from 7.95M of 8.4M; f16: 1024 bytes, from 4.2M
 of 4.3M; f32: 2048 bytes, from 2.1M of 2.2M). Only the rows the lists name
 are written; the oracle runs on a compact copy of those rows with the
 lists renumbered, so the host holds no multi-GiB arrays. Paths: one-token
-decode (chunk, slab, f16 and f32 kernels), the fused step appending at the
-cache's last position, and a prefill-sized launch (band + slab kernels). A
+decode (chunk, slab, f16, f32 and general-shape kernels), the fused step
+and q4_hip_kv_append_d appending at the cache's last position, and a
+prefill-sized launch (band + slab kernels). A
 byte offset computed in 32 bits would read or write the wrong rows here."""
 import ctypes
 
@@ -90,6 +91,7 @@ def _setup(rt, oracle, rng, kind, n_tok, pool_n):
     (q4kv.KV_Q8, 32, 1),    # slab kernel (16 query heads per KV head)
     (q4kv.KV_F16, 16, 1),   # f16 kernel
     (q4kv.KV_F32, 16, 1),   # f32 kernel
+    (q4kv.KV_Q8, 40, 1),    # general-shape kernel (20 query heads per KV head)
     (q4kv.KV_Q8, 16, 600),  # prefill-sized: band + slab kernels
 ])
 def test_decode_past_4gib(rt, oracle, kind, n_head, n_tok):
@@ -152,3 +154,34 @@ def test_step_appends_past_4gib(rt, oracle):
                        width=WIDTH, tok_stride=N_KVH * WIDTH, kvh_stride=WIDTH,
                        max_kv=cache.used.size)
     assert_attn_close(got, want, what="past 4 GiB step")
+
+
+@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
+def test_kv_append_d_past_4gib(rt, oracle, kind):
+    """q4_hip_kv_append_d at the device position max_kv - 1 (byte offset
+    past 2^32): the bytes land there, bit-exact, and the rows beside it are
+    untouched."""
+    note(f"large cache kv_append_d kind={kind}")
+    bpt, max_kv, _ = _layout(kind)
+    rng = np.random.default_rng(9700 + kind)
+    pos = max_kv - 1
+    kn, vn = heads(rng, (N_KVH,)), heads(rng, (N_KVH,))
+    dk, dv = rt.alloc(max_kv * bpt), rt.alloc(max_kv * bpt)
+    owned = [dk, dv]
+    try:
+        guard = np.full(bpt, 0xA5, np.uint8)
+        for d in (dk, dv):
+            rt.h2d(d + (pos - 1) * bpt, guard)
+        dkn, dvn = rt.upload(kn), rt.upload(vn)
+        owned += [dkn, dvn]
+        rt.lib.q4_hip_pos_push(pos)
+        assert rt.lib.q4_hip_kv_append_d(dk, dv, dkn, dvn, N_KVH * HD, bpt, kind)
+        rt.sync()
+        krows = rt.download(dk + (pos - 1) * bpt, 2 * bpt)
+        vrows = rt.download(dv + (pos - 1) * bpt, 2 * bpt)
+    finally:
+        for p in owned:
+            rt.free(p)
+    assert np.array_equal(krows[bpt:], oracle.encode(kn, kind))
+    assert np.array_equal(vrows[bpt:], oracle.encode(vn, kind))
+    assert np.array_equal(krows[:bpt], guard) and np.array_equal(vrows[:bpt], guard)
