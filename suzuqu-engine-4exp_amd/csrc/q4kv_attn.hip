@@ -3149,18 +3149,23 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
     const bool h16 = KIND == Q4KV_F16 && hd == 256u && gqa <= 16u && rows16 && h16_enabled();
     const bool f32w = KIND == Q4KV_F32 && hd == 256u && gqa <= 16u && rows16 && f32w_enabled();
     if (h16 || f32w) {
-        /* one pass of every wave per split; prefill-sized launches stream
-         * their passes through fewer splits */
+        /* splits of whole passes, as many as fill the chip's resident
+         * workgroup slots once (choose_split, as the chunk kernel); launches
+         * beyond that size (prefill) stream their passes through fewer
+         * splits */
         const uint32_t hg = h16 && gqa > 8u ? 2u : 1u, ne = 4u / hg * 16u;
         const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
-        uint32_t S = (uint64_t)n_items * s_full <= SLAB_MAX_WG ? s_full
-                     : n_items >= SLAB_MAX_WG                  ? 1u
-                                                               : SLAB_MAX_WG / n_items;
-        if (S < 1u) S = 1u;
-        if (S > COMB_MAXS) S = COMB_MAXS;
-        const size_t per = (size_t)gqa * PSTRIDE;
-        while (S > 1u && (size_t)n_items * S * per > cap) S--;
-        if (!have_part) S = 1u;
+        uint32_t S, cps;
+        if ((uint64_t)n_items * s_full <= SLAB_MAX_WG) {
+            choose_split(n_items, s_full, gqa, have_part, cap, S, cps);
+        } else {
+            S = n_items >= SLAB_MAX_WG ? 1u : SLAB_MAX_WG / n_items;
+            if (S < 1u) S = 1u;
+            if (S > COMB_MAXS) S = COMB_MAXS;
+            const size_t per = (size_t)gqa * PSTRIDE;
+            while (S > 1u && (size_t)n_items * S * per > cap) S--;
+            if (!have_part) S = 1u;
+        }
         pl.h16 = h16;
         pl.f32w = f32w;
         pl.hg = hg;
@@ -3172,14 +3177,21 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
     const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
     const bool prefill_sized = (uint64_t)n_items * s_full > SLAB_MAX_WG;
     if (KIND == Q4KV_Q8 && hd == 256u && rows16 && slab_takes(gqa, prefill_sized)) {
-        /* many items (prefill): fewer splits, each wave streaming its passes */
-        uint32_t S = !prefill_sized ? s_full : n_items >= SLAB_MAX_WG ? 1u : SLAB_MAX_WG / n_items;
-        if (S < 1u) S = 1u;
-        {
+        /* decode: splits of whole passes filling the resident slots once
+         * (choose_split); many items (prefill): fewer splits, each wave
+         * streaming its passes */
+        uint32_t S, cps;
+        if (!prefill_sized) {
+            choose_split(n_items, s_full, gqa, have_part, cap, S, cps);
+        } else {
+            S = n_items >= SLAB_MAX_WG ? 1u : SLAB_MAX_WG / n_items;
+            if (S < 1u) S = 1u;
             if (S > COMB_MAXS) S = COMB_MAXS;
             const size_t per = (size_t)gqa * PSTRIDE;
             while (S > 1u && (size_t)n_items * S * per > cap) S--; /* waves then loop */
             if (!have_part) S = 1u;
+        }
+        {
             pl.slab = true;
             pl.hg = hg;
             pl.S = S;
