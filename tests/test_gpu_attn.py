@@ -75,6 +75,66 @@ def test_null_gate_rejected_by_reference_entry_points(rt):
     assert not rt.lib.q4_hip_qsa_decode_n(p, p, p, p, p, 2, 1, 512, 1, 0, 4, 0.17, 0)
 
 
+def test_entry_points_refuse_null_and_empty_arguments(rt):
+    """The reference's error convention (src/q4_rocm.cu:20-28, 7253-7254):
+    false, never a launch, for null buffers, zero counts and bad shapes; the
+    output buffer stays untouched."""
+    note("argument refusals")
+    lib, p = rt.lib, rt.alloc(1 << 20)
+    out = _out(rt, 4 * 16 * 256)
+    dn = lib.q4_hip_qsa_decode_n
+    assert not dn(None, p, p, p, out, 16, 2, 256, 1, 0, 8, 0.06, 2)   # q
+    assert not dn(p, None, p, p, out, 16, 2, 256, 1, 0, 8, 0.06, 2)   # K cache
+    assert not dn(p, p, None, p, out, 16, 2, 256, 1, 0, 8, 0.06, 2)   # V cache
+    assert not dn(p, p, p, p, None, 16, 2, 256, 1, 0, 8, 0.06, 2)     # out
+    assert not dn(p, p, p, p, out, 16, 2, 256, 0, 0, 8, 0.06, 2)      # n_tok 0
+    assert not dn(p, p, p, p, out, 0, 2, 256, 1, 0, 8, 0.06, 2)       # n_head 0
+    assert not dn(p, p, p, p, out, 16, 0, 256, 1, 0, 8, 0.06, 2)      # n_kvh 0
+    assert not dn(p, p, p, p, out, 16, 2, 0, 1, 0, 8, 0.06, 2)        # hd 0
+    assert not dn(p, p, p, p, out, 16, 3, 256, 1, 0, 8, 0.06, 2)      # n_head % n_kvh
+    assert not dn(p, p, p, p, out, 16, 2, 256, 1, 0, 8, 0.06, 3)      # width kind
+    assert not lib.q4_hip_qsa_decode(p, p, p, p, out, 16, 2, 256, 0, 8, 0.06, 2)  # n_kv 0
+    ik = lib.q4_hip_qsa_decode_idx_kv
+    assert not ik(p, p, p, None, out, None, 4, 8, 4, 16, 2, 256, 1, 8, 0.06, 2)  # idx
+    assert not ik(p, p, p, None, out, p, 0, 8, 4, 16, 2, 256, 1, 8, 0.06, 2)     # width 0
+    assert not ik(p, p, p, None, out, p, 4, 8, 4, 16, 2, 256, 0, 8, 0.06, 2)     # n_tok 0
+    assert not lib.q4_hip_qsa_decode_batch(None, 1, 16, 2, 256, 0.06, 2, 8)
+    assert not lib.q4_hip_qsa_decode_batch(p, 0, 16, 2, 256, 0.06, 2, 8)
+    assert not lib.q4_hip_qsa_decode_batch(p, 1, 16, 2, 256, 0.06, 2, 0)
+    assert not lib.q4_hip_qsa_step_batch(None, 1, 16, 2, 256, 0.06, 2, 8)
+    assert not lib.q4_hip_qsa_step_batch(p, 0, 16, 2, 256, 0.06, 2, 8)
+    rt.sync()
+    assert np.isnan(rt.download(out, 4 * 16 * 256, np.float32)).all()
+    rt.free(p)
+    rt.free(out)
+
+
+def test_no_visible_position_gives_zero_rows(rt):
+    """max_kv 0: no position is visible, so every output row is 0 (sum 0 ->
+    out 0, src/q4_rocm.cu:6968-7013), for the dense and the listed entry
+    points."""
+    note("max_kv 0")
+    rng = np.random.default_rng(77)
+    q = heads(rng, (1, 16))
+    dq, dg = rt.upload(q), rt.upload(np.zeros_like(q))
+    kv = rt.alloc(64 * 544)
+    rt.h2d(kv, np.zeros(64 * 544, np.uint8))
+    sel = rt.upload(np.arange(2 * 8, dtype=np.int32))
+    for dense in (True, False):
+        do = _out(rt, q.nbytes)
+        if dense:
+            ok = rt.lib.q4_hip_qsa_decode_n(dq, kv, kv, dg, do, 16, 2, 256, 1, 5, 0, 1.0 / 16, 2)
+        else:
+            ok = rt.lib.q4_hip_qsa_decode_idx_kv(dq, kv, kv, None, do, sel, 8, 16, 8, 16, 2,
+                                                 256, 1, 0, 1.0 / 16, 2)
+        assert ok, dense
+        rt.sync()
+        assert not rt.download(do, q.nbytes, np.float32).any(), dense
+        rt.free(do)
+    for x in (dq, dg, kv, sel):
+        rt.free(x)
+
+
 # ------------------------------------------------- config 0: dense decode, ctx 4096
 def test_config0_dense_decode_after_append(rt, oracle):
     note("config0 dense 4097")
