@@ -3176,7 +3176,16 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
     const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
     const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
     const bool prefill_sized = (uint64_t)n_items * s_full > SLAB_MAX_WG;
-    if (KIND == Q4KV_Q8 && hd == 256u && rows16 && slab_takes(gqa, prefill_sized)) {
+    bool slab = KIND == Q4KV_Q8 && hd == 256u && rows16 && slab_takes(gqa, prefill_sized);
+    if (!slab && KIND == Q4KV_Q8 && hd == 256u && rows16 && gqa <= 8u && slab_mode() == 1) {
+        /* many items (batched decode): where the chunk kernel would walk
+         * three or more chunks per split, the slab kernel's barrier-free
+         * passes measure faster (32 sequences: 30.7 vs 33.6 us per step) */
+        uint32_t S0, cps0;
+        choose_split(n_items, (max_n + 63u) / 64u, gqa, have_part, cap, S0, cps0);
+        slab = cps0 >= db_min_chunks();
+    }
+    if (slab) {
         /* decode: splits of whole passes filling the resident slots once
          * (choose_split); many items (prefill): fewer splits, each wave
          * streaming its passes */
