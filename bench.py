@@ -705,7 +705,8 @@ def config_out(b, steps=100, sets=4, n_embd=4096):
 
 def config_gqa12(b, steps=200, n_head=24):
     """The reference's production head layout (24 query heads over 2 KV heads,
-    12 per KV head; SURVEY's model shape) on config 1's 12-layer decode step:
+    12 per KV head, the model the reference ships for) on config 1's 12-layer
+    decode step:
     q8_0 append + sparse attention over the same caches and selections,
     through q4_hip_qsa_step_batch (one fused launch + the merge)."""
     rt, lib = b.rt, b.lib

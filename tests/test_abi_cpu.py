@@ -43,7 +43,7 @@ def test_host_layout_functions():
     assert lib.q4kv_kind_of(b"q8") == 2 and lib.q4kv_kind_of(b"anything") == 2
     assert [lib.q4kv_token_bytes(k, 2, 256) for k in (2, 1, 0)] == [544, 1024, 2048]
     assert [lib.q4kv_tag(k) for k in (2, 1, 0)] == [8, 2, 4]
-    # 12 QSA layers at ctx 262144 in q8_0: 3.2 GiB (reference DESIGN.md:62-64)
+    # 12 QSA layers at ctx 262144 in q8_0: 3.2 GiB (the reference repository's DESIGN.md:62-64)
     gib = lib.q4kv_cache_bytes(2, 12, 2, 256, 262144) / 2**30
     assert abs(gib - 3.19) < 0.01
     assert abs(lib.q4kv_cache_bytes(2, 12, 2, 256, 65536) / 2**30 - 0.80) < 0.01
