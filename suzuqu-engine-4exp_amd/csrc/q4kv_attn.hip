@@ -856,7 +856,10 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
 
     TRACE(0);
     const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    /* the wave index in a scalar register: the LDS addresses derived from it
+     * are then uniform without a readfirstlane per row DMA */
+    const uint32_t tid = threadIdx.x, lane = tid & 63u,
+                   wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t gqa = a.n_head / a.n_kvh;
     const uint32_t kh = item % a.n_kvh;
     const Item it = resolve_item<MODE>(a, item);
@@ -867,6 +870,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     const uint32_t mrow = lane & 15u, jg = lane >> 4;
     const bool lo_row = mrow >= 8u;
     const size_t rstride = (size_t)a.n_kvh * ROWB; /* bytes per token */
+    const uint32_t rstride32 = a.n_kvh * ROWB;     /* < 2^32: one 32 x 32 -> 64-bit mad per row */
     /* even q8_0 blocks: byte offset of this lane's first dword in the block
      * pair, and the perm selector of its second (identity except group 3) */
     const uint32_t k_eoff = jg < 3u ? 4u + 8u * jg : 28u;
@@ -971,7 +975,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 const uint32_t e0 = (wave + 4u * u) * 64u, e = e0 + lane;
                 if (u < 4u || wave == 0) {
                     const uint32_t r = e / NCH, q = e - r * NCH;
-                    const size_t off = (size_t)(pidx[u] < 0 ? 0 : pidx[u]) * rstride + q * 16u;
+                    const uint64_t off = (uint64_t)(uint32_t)(pidx[u] < 0 ? 0 : pidx[u]) * rstride32 + q * 16u;
                     (void)r;
                     dma16(kbase + off, kr + e0 * 16u);
                     dma16(vbase + off, vr + e0 * 16u);
