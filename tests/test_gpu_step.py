@@ -197,16 +197,18 @@ def test_step_batch_more_heads_position_anywhere(rt, oracle, kind):
     _check(rt, oracle, items, ctx, kind, what=f"24 heads, position anywhere, width {kind}")
 
 
-@pytest.mark.parametrize("kind", [q4kv.KV_Q8, q4kv.KV_F16, q4kv.KV_F32])
-def test_step_batch_graph_replays(rt, oracle, kind):
+@pytest.mark.parametrize("kind,n_seq", [(q4kv.KV_Q8, 3), (q4kv.KV_F16, 3), (q4kv.KV_F32, 3),
+                                        (q4kv.KV_Q8, 32), (q4kv.KV_F16, 32)])
+def test_step_batch_graph_replays(rt, oracle, kind, n_seq):
     """q4_hip_qsa_step_batch captured once into a graph and replayed four
     times, each replay a new decode position with new rows, queries and
     selections written between replays (descriptors included): every replay
     matches the oracle over the cache as appended so far, and the caches end
-    byte-identical to the oracle's appends."""
-    note(f"graph-captured step_batch kind={kind}")
-    rng = np.random.default_rng(970 + kind)
-    n_seq, ctx, base = 3, 6000, 5000
+    byte-identical to the oracle's appends. 3 sequences take one chunk or
+    pass per split; 32 take several (q8_0: the slab kernel)."""
+    note(f"graph-captured step_batch kind={kind} n_seq={n_seq}")
+    rng = np.random.default_rng(970 + kind + n_seq)
+    ctx, base = 6000, 5000
     bpt = q4kv.token_bytes(kind, N_KVH, HD)
     lib = rt.lib
     hk, hv, kcs, vcs = [], [], [], []
