@@ -1349,7 +1349,10 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float kst[PREP ? 256u : 1u];
 
     TRACEW(0);
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    /* the wave index in a scalar register: the LDS addresses derived from it
+     * are then uniform without a readfirstlane per row DMA */
+    const uint32_t tid = threadIdx.x, lane = tid & 63u,
+                   wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t slab = wave / HG, hg = wave % HG;
     const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
     const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
@@ -1357,6 +1360,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     const uint32_t c = lane & 15u, jg = lane >> 4; /* MFMA column / row, k-group */
     const float nsel = c >= 8u ? -1.f : 0.f;
     const size_t rstride = (size_t)a.n_kvh * ROWB;
+    const uint32_t rstride32 = a.n_kvh * ROWB; /* < 2^32: one 32 x 32 -> 64-bit mad per row */
     const uint8_t *kbase = it.kc + (size_t)kh * ROWB, *vbase = it.vc + (size_t)kh * ROWB;
     const uint32_t k_eoff = jg < 3u ? 4u + 8u * jg : 28u;
     const uint32_t k_esel = jg == 3u ? 0x05040302u : 0x07060504u;
@@ -1427,7 +1431,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
                 const uint32_t e = u * 64u + lane;
                 const uint32_t r = e / NCH, q = e - r * NCH;
                 const int32_t pr = __builtin_amdgcn_ds_bpermute((int)((r & 31u) * 4u), pos);
-                const size_t off = (size_t)(pr < 0 ? 0 : pr) * rstride + q * 16u;
+                const uint64_t off = (uint64_t)(uint32_t)(pr < 0 ? 0 : pr) * rstride32 + q * 16u;
                 if (u < 8u || lane < 32u) {
                     dma16(kbase + off, krow + u * 1024u);
                     dma16(vbase + off, vrow + u * 1024u);
