@@ -3,17 +3,13 @@ slab, band), against the oracle (|got - ref| <= 2e-3 + 1e-3*|ref|).
 
 The kernels carry Q as fp16 hi/lo parts, so |q| (times the softmax scale
 where a kernel folds it in) must stay inside fp16's range; within that
-range the results must not depend on the magnitude. The slab kernel also
-folds the +1152 bias of its int8 -> fp16 K operands into one MFMA whose
-operand is -1152 x (the sum of a 32-dimension block of q x scale), split
-into fp16 parts: here one block of every head sums to +704 and another to
--640 (about +63 and -58 after the scale, so -1152 x that is beyond fp16's
-65504), which that operand must still represent.
-
-Within fp16's range the results must not depend on the magnitude: the
-slab kernel's K operands are exact (no bias left in the products); the chunk
-kernel removes the bias through the accumulator input of each block's
-MFMA."""
+range the results must not depend on the magnitude. Here one 32-dimension
+block of every head sums to about +704 and another to about -640 (about +63
+and -58 after the scale): a kernel that folded the +1152 bias of its
+int8 -> fp16 K operands into a product with those sums (-1152 x 63 is
+beyond fp16's 65504) would fail. The slab kernel's K operands are exact (no
+bias left in the products); the chunk kernel removes the bias through the
+accumulator input of each block's MFMA, in fp32."""
 import numpy as np
 import pytest
 
