@@ -389,6 +389,18 @@ __device__ static inline float row16_sum(float v) {
     return v + dppf<0x140>(v);
 }
 
+/* Sum and maximum over the 64 lanes of a wave (every lane gets the result). */
+__device__ static inline float wave_sum64(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ static inline float wave_max64(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
 /* Partial row layout: [m, l, 256 columns in MFMA output order]. */
 #define PSTRIDE 258u
 
@@ -942,12 +954,6 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                 *(const float4 *)(it.q + (size_t)h * 512u + 256u + d);
         }
     }
-    if (IS_STEP(MODE) && s == 0u && it.pos_new < it.max_kv && tid < 128u) {
-        int q[4];
-        const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
-        uint8_t *row = (uint8_t *)(tid < 64u ? kbase : vbase) + (size_t)it.pos_new * rstride;
-        q8_lane_store(row + 34u * ((tid >> 3) & 7u), tid & 7u, d, q);
-    }
     h8_t qa[8];
     /* K operands stay biased by +1152 (the exponent trick's 1024 + 128);
      * qbias[b] = qa[b] x (-1152) is the MFMA accumulator input that removes
@@ -1240,6 +1246,15 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             stg((fv2 *)(pbase + tid * PSTRIDE), (fv2){s_ml[0][tid], s_ml[1][tid]});
         }
     }
+    /* MODE_STEP: split 0 writes the quantised rows last, so no wait inside
+     * the kernel covers these stores (the chunks that list the position
+     * took the same bytes in LDS) */
+    if (IS_STEP(MODE) && s == 0u && it.pos_new < it.max_kv && tid < 128u) {
+        int q[4];
+        const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
+        uint8_t *row = (uint8_t *)(tid < 64u ? kbase : vbase) + (size_t)it.pos_new * rstride;
+        q8_lane_store(row + 34u * ((tid >> 3) & 7u), tid & 7u, d, q);
+    }
     TRACE(12);
 }
 
@@ -1445,20 +1460,6 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     bool any = n_pass > 0u ? issue(0u, ne, pos) : false;
     TRACEW(1);
 
-    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
-        int q[4];
-        float d;
-        uint8_t *row;
-        if (!PREP) { /* with the prep the K row is written once prepared */
-            d = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
-            row = (uint8_t *)kbase + (size_t)it.pos_new * rstride;
-            q8_lane_store(row + 34u * (lane >> 3), lane & 7u, d, q);
-        }
-        d = q8_lane_quant(nv[0], nv[1], nv[2], nv[3], q);
-        row = (uint8_t *)vbase + (size_t)it.pos_new * rstride;
-        q8_lane_store(row + 34u * (lane >> 3), lane & 7u, d, q);
-    }
-
     if (PREP) {
         /* RMSNorm + RoPE of the query heads (wave w: heads w, w + 4, ..) and,
          * by wave 0, of the new key row, at the token's position, through the
@@ -1482,12 +1483,6 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         const uint32_t off = 32u * (lane >> 3) + 4u * (lane & 7u);
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) nk[i] = kst[off + i];
-        if (s == 0u && wave == 0u && it.pos_new < it.max_kv) {
-            int q[4];
-            const float d = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
-            uint8_t *row = (uint8_t *)kbase + (size_t)it.pos_new * rstride;
-            q8_lane_store(row + 34u * (lane >> 3), lane & 7u, d, q);
-        }
     }
 
     /* ---- Q^T operands, built once per workgroup ---- */
@@ -1752,6 +1747,17 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             if (t == 0u && jq == 0u) stg((fv2 *)pb, (fv2){Mh, L});
         }
     }
+    /* MODE_STEP: split 0 writes the quantised rows (K after its prep) last,
+     * so no wait inside the kernel covers these stores */
+    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
+        int q[4];
+        float d = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
+        q8_lane_store((uint8_t *)kbase + (size_t)it.pos_new * rstride + 34u * (lane >> 3),
+                      lane & 7u, d, q);
+        d = q8_lane_quant(nv[0], nv[1], nv[2], nv[3], q);
+        q8_lane_store((uint8_t *)vbase + (size_t)it.pos_new * rstride + 34u * (lane >> 3),
+                      lane & 7u, d, q);
+    }
     TRACEW(10);
 }
 
@@ -1878,11 +1884,6 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
     };
     int32_t pos = -1;
     bool any = n_pass > 0u ? issue(0u, pos) : false;
-
-    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
-        stg((u2_t *)(kbase + (size_t)it.pos_new * rstride + 8u * lane), (u2_t){nk2[0], nk2[1]});
-        stg((u2_t *)(vbase + (size_t)it.pos_new * rstride + 8u * lane), (u2_t){nv2[0], nv2[1]});
-    }
 
     /* ---- Q^T operands, built once per workgroup ---- */
 #pragma unroll
@@ -2045,6 +2046,11 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
             if (t == 0u && jq == 0u) stg((fv2 *)pb, (fv2){Mh, L});
         }
     }
+    /* MODE_STEP: split 0 writes the new rows last (no wait covers them) */
+    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
+        stg((u2_t *)(kbase + (size_t)it.pos_new * rstride + 8u * lane), (u2_t){nk2[0], nk2[1]});
+        stg((u2_t *)(vbase + (size_t)it.pos_new * rstride + 8u * lane), (u2_t){nv2[0], nv2[1]});
+    }
 }
 
 /* ------------------------------------------------------------------------
@@ -2095,9 +2101,13 @@ __global__ __launch_bounds__(256, 2) void qsa_f32w_k(AttnArgs a) {
     const uint32_t j1 = (uint32_t)(((uint64_t)(s + 1u) * n) / a.S);
     const uint32_t n_pass = j1 > j0 ? (j1 - j0 + NE - 1u) / NE : 0u;
 
-    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
-        stg((f4_t *)(kbase + (size_t)it.pos_new * rstride) + lane, ldg((const f4_t *)it.knew + lane));
-        stg((f4_t *)(vbase + (size_t)it.pos_new * rstride) + lane, ldg((const f4_t *)it.vnew + lane));
+    /* MODE_STEP: split 0's wave 0 holds the new rows (lane l: floats
+     * 4 l .. 4 l + 3) and writes them last, so no wait covers the stores */
+    const bool step_wr = IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv;
+    f4_t nk4 = {0.f, 0.f, 0.f, 0.f}, nv4 = nk4;
+    if (step_wr) {
+        nk4 = ldg((const f4_t *)it.knew + lane);
+        nv4 = ldg((const f4_t *)it.vnew + lane);
     }
     for (uint32_t e = tid; e < 16u * 256u; e += 256u) {
         const uint32_t h = e >> 8, d = e & 255u;
@@ -2223,6 +2233,10 @@ __global__ __launch_bounds__(256, 2) void qsa_f32w_k(AttnArgs a) {
             stg(pbase + h * PSTRIDE + 2u + d, x);
             if (d == 0u) stg((fv2 *)(pbase + h * PSTRIDE), (fv2){M, L});
         }
+    }
+    if (step_wr) {
+        stg((f4_t *)(kbase + (size_t)it.pos_new * rstride) + lane, nk4);
+        stg((f4_t *)(vbase + (size_t)it.pos_new * rstride) + lane, nv4);
     }
 }
 
@@ -2649,41 +2663,67 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
 /* Merge the S split partials of one (item, head): weights 2^(m_s - M) over
  * splits with l_s > 0, then the sigmoid gate (src/q4_rocm.cu:6968-7013).
  * Thread c owns output column c. For S <= COMB_REG every partial load
- * (columns and the wave-uniform m_s, l_s) is issued before the first is used
- * and the merge needs neither LDS nor barriers: one memory round trip. */
+ * (its columns, and one split's m_s, l_s per lane) is issued before the
+ * first is used and the merge needs neither LDS nor barriers. */
 #define COMB_MAXS 1024u
 #define COMB_REG 64u
 
 /* R >= S: all S partials in registers (indices past S re-read split S-1 and
- * get weight 0). */
+ * get weight 0). Lane k of every wave loads split k's (m, l) (S <= 64), so a
+ * thread has R + 2 loads in flight (within the 63 the vmcnt counter holds,
+ * one memory round trip); the weights 2^(m_k - M) are formed once per lane
+ * and read back per split with v_readlane. xv = *xp is loaded in the same
+ * round trip (the gate value, where there is one). */
 template <uint32_t R>
 __device__ static inline float comb_reg(const float *pb, size_t sst, uint32_t S, uint32_t col,
-                                        float &L) {
-    float v[R], m[R], l[R];
-    /* a per-lane zero the compiler cannot fold: keeps the uniform m_s, l_s
-     * loads on the vector path, issued with the column loads (scalar loads
-     * would be waited for in small groups) */
-    uint32_t z;
-    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+                                        float &L, const float *xp, float &xv) {
+    static_assert(R <= 64u, "one split per lane");
+    const uint32_t lane = threadIdx.x & 63u;
+    const float *pm = pb + (lane < S ? lane : S - 1u) * sst;
+    const float mk = ldg(pm), lk = ldg(pm + 1u);
+    float v[R];
 #pragma unroll
-    for (uint32_t k = 0; k < R; k++) {
-        const float *p = pb + (k < S ? k : S - 1u) * sst;
-        m[k] = ldg(p + z);
-        l[k] = ldg(p + 1u + z);
-        v[k] = ldg(p + 2u + col);
-    }
-    float M = -INFINITY;
+    for (uint32_t k = 0; k < R; k++) v[k] = ldg(pb + (k < S ? k : S - 1u) * sst + 2u + col);
+    xv = ldg(xp);
+    /* every load above is issued before the wait for (m, l) */
+    __builtin_amdgcn_sched_barrier(0);
+    const bool ok = lane < S && lk > 0.f;
+    const float M = wave_max64(ok ? mk : -INFINITY);
+    const float w = ok ? __builtin_amdgcn_exp2f(mk - M) : 0.f;
+    L = wave_sum64(w * lk);
+    float acc = 0.f;
 #pragma unroll
     for (uint32_t k = 0; k < R; k++)
-        if (k < S && l[k] > 0.f) M = fmax2(M, m[k]);
-    float acc = 0.f;
+        acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), (int)k)) * v[k];
+    return acc;
+}
+
+/* The merged (unnormalised) column col of one (item, head) from its S split
+ * partials at pb (stride sst), L the merged denominator; xv = *xp, loaded
+ * with the partials. */
+__device__ static inline float comb_cols(const float *pb, size_t sst, uint32_t S, uint32_t col,
+                                         float &L, const float *xp, float &xv) {
+    if (S <= 8u) return comb_reg<8>(pb, sst, S, col, L, xp, xv);
+    if (S <= 16u) return comb_reg<16>(pb, sst, S, col, L, xp, xv);
+    if (S <= 20u) return comb_reg<20>(pb, sst, S, col, L, xp, xv);
+    if (S <= 24u) return comb_reg<24>(pb, sst, S, col, L, xp, xv);
+    if (S <= 32u) return comb_reg<32>(pb, sst, S, col, L, xp, xv);
+    if (S <= 36u) return comb_reg<36>(pb, sst, S, col, L, xp, xv);
+    if (S <= 48u) return comb_reg<48>(pb, sst, S, col, L, xp, xv);
+    if (S <= COMB_REG) return comb_reg<COMB_REG>(pb, sst, S, col, L, xp, xv);
+    /* long split lists: two passes over the partials */
+    xv = ldg(xp);
+    float M = -INFINITY, acc = 0.f;
     L = 0.f;
-#pragma unroll
-    for (uint32_t k = 0; k < R; k++) {
-        const float e = __builtin_amdgcn_exp2f(m[k] - M);
-        const float w = (k < S && l[k] > 0.f) ? e : 0.f;
-        L += w * l[k];
-        acc += w * v[k];
+    for (uint32_t sp = 0; sp < S; sp++)
+        if (ldg(pb + sp * sst + 1u) > 0.f) M = fmax2(M, ldg(pb + sp * sst));
+    for (uint32_t sp = 0; sp < S; sp++) {
+        const float l = ldg(pb + sp * sst + 1u);
+        if (l > 0.f) {
+            const float w = __builtin_amdgcn_exp2f(ldg(pb + sp * sst) - M);
+            L += w * l;
+            acc += w * ldg(pb + sp * sst + 2u + col);
+        }
     }
     return acc;
 }
@@ -2697,33 +2737,15 @@ __global__ __launch_bounds__(256) void qsa_comb_k(AttnArgs a) {
     const uint32_t dim = col_dim<KIND>(tid);
     const bool dvalid = dim < hd;
     const uint32_t col = dvalid ? tid : 0u;
-    float L = 0.f, acc = 0.f;
-    if (S <= 8u) acc = comb_reg<8>(pb, sst, S, col, L);
-    else if (S <= 16u) acc = comb_reg<16>(pb, sst, S, col, L);
-    else if (S <= 20u) acc = comb_reg<20>(pb, sst, S, col, L);
-    else if (S <= 24u) acc = comb_reg<24>(pb, sst, S, col, L);
-    else if (S <= 32u) acc = comb_reg<32>(pb, sst, S, col, L);
-    else if (S <= 36u) acc = comb_reg<36>(pb, sst, S, col, L);
-    else if (S <= 48u) acc = comb_reg<48>(pb, sst, S, col, L);
-    else if (S <= COMB_REG) acc = comb_reg<COMB_REG>(pb, sst, S, col, L);
-    else {
-        /* long split lists: two passes over the partials */
-        float M = -INFINITY;
-        for (uint32_t sp = 0; sp < S; sp++)
-            if (ldg(pb + sp * sst + 1u) > 0.f) M = fmax2(M, ldg(pb + sp * sst));
-        for (uint32_t sp = 0; sp < S; sp++) {
-            const float l = ldg(pb + sp * sst + 1u);
-            if (l > 0.f) {
-                const float w = __builtin_amdgcn_exp2f(ldg(pb + sp * sst) - M);
-                L += w * l;
-                acc += w * ldg(pb + sp * sst + 2u + col);
-            }
-        }
-    }
-    if (!dvalid) return;
     const Item it = resolve_item<MODE>(a, item);
+    /* the gate value is loaded with the partials (any readable word when
+     * there is no gate) */
+    const float *gp = it.gate && dvalid ? it.gate + (size_t)g * hd + dim : pb;
+    float L, gv;
+    const float acc = comb_cols(pb, sst, S, col, L, gp, gv);
+    if (!dvalid) return;
     float r = L > 0.f ? acc / L : 0.f;
-    if (it.gate) r *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)g * hd + dim)));
+    if (it.gate) r *= 1.f / (1.f + expf(-gv));
     stg(it.out + (size_t)g * hd + dim, r);
 }
 
@@ -2753,31 +2775,11 @@ __global__ __launch_bounds__(256) void qsa_comb_gemv_k(AttnArgs a, const q4kv_ou
     if (S > 1u) {
         const float *pb = a.part + ((size_t)item * S * gqa + g) * PSTRIDE;
         const size_t sst = (size_t)gqa * PSTRIDE;
-        float L = 0.f, acc;
-        if (S <= 8u) acc = comb_reg<8>(pb, sst, S, tid, L);
-        else if (S <= 16u) acc = comb_reg<16>(pb, sst, S, tid, L);
-        else if (S <= 20u) acc = comb_reg<20>(pb, sst, S, tid, L);
-        else if (S <= 24u) acc = comb_reg<24>(pb, sst, S, tid, L);
-        else if (S <= 32u) acc = comb_reg<32>(pb, sst, S, tid, L);
-        else if (S <= 36u) acc = comb_reg<36>(pb, sst, S, tid, L);
-        else if (S <= 48u) acc = comb_reg<48>(pb, sst, S, tid, L);
-        else if (S <= COMB_REG) acc = comb_reg<COMB_REG>(pb, sst, S, tid, L);
-        else {
-            float M = -INFINITY;
-            acc = 0.f;
-            for (uint32_t sp = 0; sp < S; sp++)
-                if (ldg(pb + sp * sst + 1u) > 0.f) M = fmax2(M, ldg(pb + sp * sst));
-            for (uint32_t sp = 0; sp < S; sp++) {
-                const float l = ldg(pb + sp * sst + 1u);
-                if (l > 0.f) {
-                    const float w = __builtin_amdgcn_exp2f(ldg(pb + sp * sst) - M);
-                    L += w * l;
-                    acc += w * ldg(pb + sp * sst + 2u + tid);
-                }
-            }
-        }
+        const float *gp = it.gate ? it.gate + (size_t)g * hd + dim : pb;
+        float L, gv;
+        const float acc = comb_cols(pb, sst, S, tid, L, gp, gv);
         r = L > 0.f ? acc / L : 0.f;
-        if (it.gate) r *= 1.f / (1.f + expf(-ldg(it.gate + (size_t)g * hd + dim)));
+        if (it.gate) r *= 1.f / (1.f + expf(-gv));
         if (rb == 0) stg(it.out + (size_t)g * hd + dim, r);
     } else {
         r = ldg(it.out + (size_t)g * hd + dim); /* one split: already merged and gated */
@@ -2940,16 +2942,6 @@ __device__ static inline float any_elem(const uint8_t *row, uint32_t d) {
     return ld_f16_g(blk) * (float)(int8_t)ldg(blk + 2u + (d & 31u));
 }
 
-__device__ static inline float wave_sum64(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-__device__ static inline float wave_max64(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
 
 template <int KIND, int MODE>
 __global__ __launch_bounds__(256) void qsa_any_k(AttnArgs a) {
@@ -3249,6 +3241,9 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
             return launch_any<KIND, MODE>(a, n_items, max_n, gqa, pb);
         }
     }
+    /* the kernels resolve items from what the mode names: descriptors, or
+     * the direct arguments */
+    if (IS_BATCH(MODE) ? !a.seqs : (!a.kc || !a.vc || !a.q || !a.out)) return false;
     const bool fast = KIND == Q4KV_Q8 && a.hd == 256u && gqa <= 8u;
     /* batch modes: the caches are in device descriptors, 16-byte aligned by
      * contract */
