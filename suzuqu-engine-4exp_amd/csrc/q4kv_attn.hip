@@ -74,6 +74,9 @@ struct AttnArgs {
      * the band's unnormalised output rows are in out */
     int32_t *band_nb;
     float *band_ml;
+    /* XCD pairing (qsa_q8d256_k, 1D grid when xgrp > 0): xgrp (token, split)
+     * groups, each run by its n_kvh KV heads' workgroups on one XCD */
+    uint32_t xgrp;
 };
 
 struct Item {
@@ -867,7 +870,19 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float kst[MODE == MODE_PSTEP ? 256 : 1];
 
     TRACE(0);
-    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    if (a.xgrp) {
+        /* workgroup L runs on XCD L mod 8: group P = 8 (r / n_kvh) + L mod 8
+         * with r = L / 8 puts the n_kvh workgroups of (token, split) P on one
+         * XCD, where the lines their K/V rows share (the heads of a position
+         * are adjacent) are fetched once into its L2 */
+        const uint32_t L = blockIdx.x, r = L >> 3, kh = r % a.n_kvh;
+        const uint32_t P = (r / a.n_kvh) * 8u + (L & 7u);
+        if (P >= a.xgrp) return; /* padding of the last group row */
+        const uint32_t t = P / a.S;
+        s = P - t * a.S;
+        item = a.item0 + t * a.n_kvh + kh;
+    }
     /* the wave index in a scalar register: the LDS addresses derived from it
      * are then uniform without a readfirstlane per row DMA */
     const uint32_t tid = threadIdx.x, lane = tid & 63u,
@@ -3223,6 +3238,17 @@ static bool band_enabled(void) {
     return v != 0;
 }
 
+/* KV-head pairing on one XCD for the chunk kernel (Q4KV_XPAIR=0 turns it
+ * off, for measurement). */
+static bool xcd_pair_enabled(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_XPAIR");
+        v = (e && e[0] == '0') ? 0 : 1;
+    }
+    return v != 0;
+}
+
 /* A fused append + attention launch exists for this shape. */
 static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
     if (kind == Q4KV_F16) return hd == 256u && gqa <= 16u && h16_enabled();
@@ -3259,6 +3285,14 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         const uint32_t ni = n_items - i0 < Q4KV_MAX_GRID_Y ? n_items - i0 : Q4KV_MAX_GRID_Y;
         a.item0 = i0;
         dim3 grid(S, ni);
+        /* the chunk kernel over whole tokens: the KV heads of each (token,
+         * split) on one XCD */
+        a.xgrp = 0u;
+        if (fast && !pl.slab && !pl.h16 && !pl.f32w && xcd_pair_enabled() && a.n_kvh > 1u &&
+            ni == n_items && ni % a.n_kvh == 0u) {
+            a.xgrp = ni / a.n_kvh * S;
+            grid = dim3(8u * a.n_kvh * ((a.xgrp + 7u) / 8u), 1u);
+        }
         const bool prof = prof_armed();
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
         /* prefill through the slab kernel (one split): the shared recent
