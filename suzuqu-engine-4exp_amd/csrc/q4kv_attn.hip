@@ -74,7 +74,7 @@ struct AttnArgs {
      * the band's unnormalised output rows are in out */
     int32_t *band_nb;
     float *band_ml;
-    /* XCD pairing (qsa_q8d256_k, 1D grid when xgrp > 0): xgrp (token, split)
+    /* XCD grouping (xcd_slot; 1D grid when xgrp > 0): xgrp (token, split)
      * groups, each run by its n_kvh KV heads' workgroups on one XCD */
     uint32_t xgrp;
 };
@@ -416,6 +416,28 @@ template <int KIND> __device__ static inline uint32_t col_dim(uint32_t col) {
     return 32u * (2u * w + (t >> 1)) + 2u * n + (t & 1u);
 }
 
+/* The (split, item) of this workgroup. With a.xgrp > 0 the grid is 1D and
+ * groups the n_kvh KV heads of each (token, split) on one XCD: workgroup L
+ * runs on XCD L mod 8 (MI355X dispatches workgroups round-robin over its 8
+ * XCDs), and group P = 8 (r / n_kvh) + L mod 8 with r = L / 8 takes
+ * workgroups L of one residue mod 8. A position's head rows are adjacent, so
+ * the lines they share are fetched once into that XCD's L2. Placement only:
+ * results do not depend on it. Returns false for the padding of the last
+ * group row. */
+__device__ static inline bool xcd_slot(const AttnArgs &a, uint32_t &s, uint32_t &item) {
+    if (!a.xgrp) {
+        s = blockIdx.x;
+        item = a.item0 + blockIdx.y;
+        return true;
+    }
+    const uint32_t L = blockIdx.x, r = L >> 3, kh = r % a.n_kvh;
+    const uint32_t P = (r / a.n_kvh) * 8u + (L & 7u);
+    const uint32_t t = P / a.S;
+    s = P - t * a.S;
+    item = a.item0 + t * a.n_kvh + kh;
+    return P < a.xgrp;
+}
+
 template <int KIND, int MODE, int HG>
 __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
     constexpr uint32_t CP = KCfg<KIND>::CP;
@@ -431,7 +453,8 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
     __shared__ float s_cmax[NQW][NH], s_psum[NQW][NH];
 
     TRACE(0);
-    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    uint32_t s, item;
+    if (!xcd_slot(a, s, item)) return; /* padding of the last group row */
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t hd = a.hd, NB = hd / 32u, gqa = a.n_head / a.n_kvh;
     const uint32_t kh = item % a.n_kvh;
@@ -870,19 +893,8 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float kst[MODE == MODE_PSTEP ? 256 : 1];
 
     TRACE(0);
-    uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
-    if (a.xgrp) {
-        /* workgroup L runs on XCD L mod 8: group P = 8 (r / n_kvh) + L mod 8
-         * with r = L / 8 puts the n_kvh workgroups of (token, split) P on one
-         * XCD, where the lines their K/V rows share (the heads of a position
-         * are adjacent) are fetched once into its L2 */
-        const uint32_t L = blockIdx.x, r = L >> 3, kh = r % a.n_kvh;
-        const uint32_t P = (r / a.n_kvh) * 8u + (L & 7u);
-        if (P >= a.xgrp) return; /* padding of the last group row */
-        const uint32_t t = P / a.S;
-        s = P - t * a.S;
-        item = a.item0 + t * a.n_kvh + kh;
-    }
+    uint32_t s, item;
+    if (!xcd_slot(a, s, item)) return; /* padding of the last group row */
     /* the wave index in a scalar register: the LDS addresses derived from it
      * are then uniform without a readfirstlane per row DMA */
     const uint32_t tid = threadIdx.x, lane = tid & 63u,
@@ -1384,7 +1396,8 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u,
                    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t slab = wave / HG, hg = wave % HG;
-    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    uint32_t s, item;
+    if (!xcd_slot(a, s, item)) return; /* padding of the last group row */
     const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
     const Item it = resolve_item<MODE>(a, item);
     const uint32_t c = lane & 15u, jg = lane >> 4; /* MFMA column / row, k-group */
@@ -1821,7 +1834,8 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t slab = wave / HG, hg = wave % HG;
-    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    uint32_t s, item;
+    if (!xcd_slot(a, s, item)) return; /* padding of the last group row */
     const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
     const Item it = resolve_item<MODE>(a, item);
     const uint32_t c = lane & 15u, jg = lane >> 4;
@@ -2105,7 +2119,8 @@ __global__ __launch_bounds__(256, 2) void qsa_f32w_k(AttnArgs a) {
     float(*qT)[4][16][4] = (float(*)[4][16][4])lds;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t s = blockIdx.x, item = a.item0 + blockIdx.y;
+    uint32_t s, item;
+    if (!xcd_slot(a, s, item)) return; /* padding of the last group row */
     const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
     const Item it = resolve_item<MODE>(a, item);
     const uint32_t c = lane & 15u, jg = lane >> 4;
@@ -3238,8 +3253,8 @@ static bool band_enabled(void) {
     return v != 0;
 }
 
-/* KV-head pairing on one XCD for the chunk kernel (Q4KV_XPAIR=0 turns it
- * off, for measurement). */
+/* KV-head grouping on one XCD (xcd_slot; Q4KV_XPAIR=0 turns it off, for
+ * measurement). */
 static bool xcd_pair_enabled(void) {
     static int v = -1;
     if (v < 0) {
@@ -3285,11 +3300,13 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         const uint32_t ni = n_items - i0 < Q4KV_MAX_GRID_Y ? n_items - i0 : Q4KV_MAX_GRID_Y;
         a.item0 = i0;
         dim3 grid(S, ni);
-        /* the chunk kernel over whole tokens: the KV heads of each (token,
-         * split) on one XCD */
+        /* the chunk kernel and the batched slab decode over whole tokens: the
+         * KV heads of each (token, split) on one XCD (for the slab kernel's
+         * prefill and the f16 / f32 kernels it measured 1-2 % slower) */
         a.xgrp = 0u;
-        if (fast && !pl.slab && !pl.h16 && !pl.f32w && xcd_pair_enabled() && a.n_kvh > 1u &&
-            ni == n_items && ni % a.n_kvh == 0u) {
+        const bool grouped = pl.slab ? IS_BATCH(MODE) : (fast && !pl.h16 && !pl.f32w);
+        if (grouped && xcd_pair_enabled() && a.n_kvh > 1u && ni == n_items &&
+            ni % a.n_kvh == 0u) {
             a.xgrp = ni / a.n_kvh * S;
             grid = dim3(8u * a.n_kvh * ((a.xgrp + 7u) / 8u), 1u);
         }
