@@ -328,6 +328,11 @@ int q4kv_device_info(char *name, int name_len, int *n_cu, int *clock_khz);
  * and their summed duration in ms. */
 bool q4kv_prof_begin(int max_launches);
 int q4kv_prof_end(double *total_ms);
+/* Placement of the split-KV launches: 1 (default) runs the KV heads of each
+ * (token, split) on one XCD, 0 uses the plain (split, item) grid, -1 only
+ * queries; returns the setting. Results are identical either way (test and
+ * measurement support; no counterpart in the reference). */
+int q4kv_xcd_group(int on);
 
 #ifdef __cplusplus
 }

@@ -3253,15 +3253,19 @@ static bool band_enabled(void) {
     return v != 0;
 }
 
-/* KV-head grouping on one XCD (xcd_slot; Q4KV_XPAIR=0 turns it off, for
- * measurement). */
+/* KV-head grouping on one XCD (xcd_slot). Q4KV_XPAIR=0 starts with it off;
+ * q4kv_xcd_group switches it (measurement and tests). */
+static int g_xpair = -1;
 static bool xcd_pair_enabled(void) {
-    static int v = -1;
-    if (v < 0) {
+    if (g_xpair < 0) {
         const char *e = getenv("Q4KV_XPAIR");
-        v = (e && e[0] == '0') ? 0 : 1;
+        g_xpair = (e && e[0] == '0') ? 0 : 1;
     }
-    return v != 0;
+    return g_xpair != 0;
+}
+extern "C" int q4kv_xcd_group(int on) {
+    if (on == 0 || on == 1) g_xpair = on;
+    return xcd_pair_enabled() ? 1 : 0;
 }
 
 /* A fused append + attention launch exists for this shape. */

@@ -166,6 +166,7 @@ SIGNATURES = {
     "q4kv_use_stream": (_b, [_vp]),
     "q4kv_prof_begin": (_b, [C.c_int]),
     "q4kv_prof_end": (C.c_int, [C.POINTER(C.c_double)]),
+    "q4kv_xcd_group": (C.c_int, [C.c_int]),
     "q4_hip_kv_append_batch": (_b, [_vp, _u32, _u32, _u32, C.c_int]),
     # host layer (include/q4kv_host.h)
     "q4kv_kind_of": (C.c_int, [C.c_char_p]),
