@@ -883,8 +883,14 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     constexpr uint32_t CP = 64, ROWB = 272, NCH = 17, NLD = 5;
     /* row buffers: [K rows | V rows] each */
     __shared__ __attribute__((aligned(16))) uint8_t rowbuf[DB ? 2 : 1][2 * CP * ROWB];
-    __shared__ __attribute__((aligned(16))) float sw[8 * CP];  /* weights [head][pos] */
-    __shared__ __attribute__((aligned(16))) float vsc[8 * CP]; /* V scales [block][pos] */
+    /* DB: weights [head][pos] and V scales [block][pos], combined per P.V
+     * tile. Single buffer: the P.V A operands themselves, fp16 hi | lo of
+     * weight x V scale, [block][hi, lo][head][pos] with 72-entry rows (16-byte
+     * pad: the 16 rows a wave's operand reads touch start 4 banks apart) */
+    constexpr uint32_t AROW = 72;
+    __shared__ __attribute__((aligned(16))) float sw[DB ? 8 * CP : 1];
+    __shared__ __attribute__((aligned(16))) float vsc[DB ? 8 * CP : 1];
+    __shared__ __attribute__((aligned(16))) _Float16 aop[DB ? 1 : 8 * 2 * 8 * AROW];
     /* raw fp32 Q rows, 1040-byte stride (4 pad floats) against bank conflicts */
     __shared__ __attribute__((aligned(16))) float qraw_s[DB ? 1 : 8 * 260];
     float *const qraw = DB ? (float *)rowbuf[DB ? 1 : 0] : qraw_s;
@@ -1098,11 +1104,13 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             }
         }
         /* V block scales, 0 for masked positions */
+        if (DB) {
 #pragma unroll
-        for (uint32_t k = 0; k < 2u; k++) {
-            const uint32_t e = tid + 256u * k, b = e >> 6, r = e & 63u;
-            const float x = ld_f16(vraw + r * ROWB + 34u * b);
-            vsc[e] = spos[r] < 0 ? 0.f : x;
+            for (uint32_t k = 0; k < 2u; k++) {
+                const uint32_t e = tid + 256u * k, b = e >> 6, r = e & 63u;
+                const float x = ld_f16(vraw + r * ROWB + 34u * b);
+                vsc[e] = spos[r] < 0 ? 0.f : x;
+            }
         }
         /* ---- scores: wave w, positions 16w .. 16w+15 ---- */
         const uint32_t r = wave * 16u + mrow;
@@ -1146,7 +1154,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         TRACE(5);
         __syncthreads();
         TRACE(6);
-        float alpha[4];
+        float alpha[4], wv[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
             const uint32_t h = (4u * jg + i) & 7u;
@@ -1158,9 +1166,33 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - ms);
             m_run[i] = mn;
             const float w = __builtin_amdgcn_exp2f(T[i] - ms);
-            if (lane < 32u) sw[(4u * jg + i) * CP + r] = w;
+            if (DB && lane < 32u) sw[(4u * jg + i) * CP + r] = w;
+            wv[i] = w;
             const float ps = row16_sum(w);
             if (mrow == 0 && jg < 2u) s_psum[wave][4u * jg + i] = ps;
+        }
+        if (!DB) {
+            /* the P.V A operands of position r, heads 4 (jg & 1) .. + 3 (lanes
+             * l and l + 32 hold the same weights): lanes < 32 blocks 0-3,
+             * lanes >= 32 blocks 4-7; each product once, split hi / lo */
+            const bool rv = spos[r] >= 0;
+            const uint32_t b0 = 4u * (lane >> 5), h0 = 4u * (jg & 1u);
+            float vsr[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; k++) vsr[k] = ld_f16(vraw + r * ROWB + 34u * (b0 + k));
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; k++) {
+                const uint32_t b = b0 + k;
+                const float vs = rv ? vsr[k] : 0.f;
+#pragma unroll
+                for (uint32_t i = 0; i < 4u; i++) {
+                    const float x = wv[i] * vs;
+                    const _Float16 hi = (_Float16)x;
+                    _Float16 *d = aop + ((b * 2u) * 8u + h0 + i) * AROW + r;
+                    d[0] = hi;
+                    d[8u * AROW] = (_Float16)(x - (float)hi);
+                }
+            }
         }
         TRACE(7);
         __syncthreads();
@@ -1191,10 +1223,14 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                     r0[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04020400u);
                     r1[k] = __builtin_amdgcn_perm(0x64646464u, x, 0x04030401u);
                 }
-                const float *sp = vsc + bb * CP + p0;
                 h8_t A;
+                if (DB) {
+                    const float *sp = vsc + bb * CP + p0;
 #pragma unroll
-                for (uint32_t i = 0; i < 8u; i++) A[i] = split_sel(wp[i] * sp[i], nsel);
+                    for (uint32_t i = 0; i < 8u; i++) A[i] = split_sel(wp[i] * sp[i], nsel);
+                } else {
+                    A = *(const h8_t *)(aop + ((bb * 2u + (lo_row ? 1u : 0u)) * 8u + g) * AROW + p0);
+                }
                 /* biased V (1152 + v): the bias leaves with A x (-1152), on the
                  * otherwise idle MFMA pipe */
                 const h8_t neg = (h8_t)((_Float16)-1152.0f);
