@@ -40,7 +40,8 @@ bool q4_hip_d2h_async(void *h, const void *d, uint64_t n); /* src/q4.h:787 */
 bool q4_hip_h2d_async(void *d, const void *h, uint64_t n); /* src/q4.h:788 */
 bool q4_hip_stream_sync(void);                /* src/q4.h:789 */
 /* f32 KV width store, n floats device-to-device (src/q4.h:851). Stream
- * ordered; the reference's version also waits for completion. */
+ * ordered, and returns once the copy has landed, as the reference's does
+ * (inside a capture it becomes a copy node). */
 bool q4_hip_copy(float *d, const float *s, uint64_t n);
 
 /* Graph capture of the compute stream (src/q4.h:782-786). */
@@ -61,7 +62,14 @@ bool q4_hip_f32_to_q8(void *dst_q8, const float *src, uint64_t n);
 /* fp32 [n] -> fp16 [n], round-to-nearest-even (src/q4.h:928). */
 bool q4_hip_f32_to_f16(void *dst_f16, const float *src, uint64_t n);
 /* Append one token's K and V (n floats each) at the device position into
- * caches with bpt bytes per token, width `kind` (src/q4.h:694-695). */
+ * caches with bpt bytes per token, width `kind` (src/q4.h:694-695).
+ * A q8_0 append of whole 256-dim head rows (bpt = n / 256 * 272) is held,
+ * not launched: the next one-token decode over the same caches performs it
+ * inside its own launch, and any other q4_hip_* / q4kv_* call launches it
+ * first, so every library call sees the appended rows, in stream order.
+ * Work the caller enqueues itself on the stream between this call and the
+ * next library call does not (it must not read the caches or overwrite k
+ * and v there). Q4KV_HOLD_APPEND=0 launches every append at once. */
 bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k, const float *v,
                         uint32_t n, uint32_t bpt, int kind);
 

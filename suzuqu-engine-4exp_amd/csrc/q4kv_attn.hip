@@ -77,6 +77,10 @@ struct AttnArgs {
     /* XCD grouping (xcd_slot; 1D grid when xgrp > 0): xgrp (token, split)
      * groups, each run by its n_kvh KV heads' workgroups on one XCD */
     uint32_t xgrp;
+    /* the held append of one token's K/V rows ([n_kvh][hd] fp32 each) at
+     * the device position *app_pos (qsa_q8d256_k with APP) */
+    const float *app_k, *app_v;
+    const int32_t *app_pos;
 };
 
 struct Item {
@@ -856,17 +860,37 @@ __device__ static inline uint32_t q8_col_of_dim(uint32_t d) {
  * stride, q8_kdim order): rows 0-7 fp16(q), rows 8-15 the residual
  * (nsel = -1); rows past gqa are zero. qbias[b] = qa[b] x (-1152) is the
  * accumulator input that removes the +1152 bias of the K operands. */
+/* Each head's q is first scaled by the power of two 2^-e that brings its
+ * largest |q| into [0.5, 1) (exact), so the fp16 parts never overflow and
+ * keep their relative precision at any magnitude of q; the score of head g
+ * is then multiplied by scale_log2 * 2^e, which build_qa stores in qm[g]
+ * (lanes of k-group 0). */
 __device__ static inline void build_qa(const float *qraw, uint32_t g, uint32_t gqa, uint32_t jg,
-                                       float nsel, h8_t (&qa)[8], f4_t (&qbias)[8]) {
+                                       float nsel, h8_t (&qa)[8], f4_t (&qbias)[8],
+                                       float scale_log2, float *qm) {
     const float *qr = qraw + (g < gqa ? g : 0u) * 260u;
-    const float qs = g < gqa ? 1.f : 0.f;
+    fv2 v[32];
+    float amax = 0.f;
 #pragma unroll
     for (uint32_t b = 0; b < 8u; b++)
 #pragma unroll
         for (uint32_t kk = 0; kk < 4u; kk++) {
-            const fv2 v = *(const fv2 *)(qr + 32u * b + q8_kdim(b, jg, 2u * kk));
-            qa[b][2u * kk] = split_sel(v[0] * qs, nsel);
-            qa[b][2u * kk + 1u] = split_sel(v[1] * qs, nsel);
+            v[4u * b + kk] = *(const fv2 *)(qr + 32u * b + q8_kdim(b, jg, 2u * kk));
+            amax = fmaxf(amax, fmaxf(fabsf(v[4u * b + kk][0]), fabsf(v[4u * b + kk][1])));
+        }
+    /* the eight lanes of head g: rows g and g + 8, k-groups 0-3 */
+    amax = fmaxf(amax, __shfl_xor(amax, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const int e = (amax > 0.f && amax <= 3.4e38f) ? __builtin_amdgcn_frexp_expf(amax) : 0;
+    const float qs = g < gqa ? __builtin_ldexpf(1.f, -e) : 0.f;
+    if (jg == 0u && (threadIdx.x & 15u) < 8u) qm[g] = __builtin_ldexpf(scale_log2, e);
+#pragma unroll
+    for (uint32_t b = 0; b < 8u; b++)
+#pragma unroll
+        for (uint32_t kk = 0; kk < 4u; kk++) {
+            qa[b][2u * kk] = split_sel(v[4u * b + kk][0] * qs, nsel);
+            qa[b][2u * kk + 1u] = split_sel(v[4u * b + kk][1] * qs, nsel);
         }
     const h8_t neg = (h8_t)((_Float16)-1152.0f);
 #pragma unroll
@@ -878,7 +902,10 @@ __device__ static inline void build_qa(const float *qraw, uint32_t g, uint32_t g
 /* DB: two row buffers, chunk c + 1's rows DMA'd while chunk c is computed
  * (for workgroups with many chunks: prefill); the Q rows are staged in the
  * second buffer, which the first chunk does not use. */
-template <int MODE, bool DB>
+/* APP: the launch also performs a held append of one token's K/V rows at
+ * the device position (the splits that list that position take its
+ * quantised bytes in LDS; split 0 of token 0 writes them to the caches). */
+template <int MODE, bool DB, bool APP = false>
 __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     constexpr uint32_t CP = 64, ROWB = 272, NCH = 17, NLD = 5;
     /* row buffers: [K rows | V rows] each */
@@ -896,9 +923,13 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     float *const qraw = DB ? (float *)rowbuf[DB ? 1 : 0] : qraw_s;
     __shared__ int32_t s_pos[DB ? 2 : 1][CP];
     __shared__ float s_cmax[4][8], s_psum[4][8], s_ml[2][8];
+    /* per-head score multipliers (scale_log2 x 2^e of the q pre-scaling) */
+    __shared__ float s_qm[8];
+    __shared__ uint32_t s_subst[2];
     __shared__ __attribute__((aligned(16))) float kst[MODE == MODE_PSTEP ? 256 : 1];
 
     TRACE(0);
+    constexpr bool STEPL = IS_STEP(MODE) || APP; /* a token's rows are appended */
     uint32_t s, item;
     if (!xcd_slot(a, s, item)) return; /* padding of the last group row */
     /* the wave index in a scalar register: the LDS addresses derived from it
@@ -907,7 +938,12 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t gqa = a.n_head / a.n_kvh;
     const uint32_t kh = item % a.n_kvh;
-    const Item it = resolve_item<MODE>(a, item);
+    Item it = resolve_item<MODE>(a, item);
+    if (APP) {
+        it.knew = a.app_k + (size_t)kh * 256u;
+        it.vnew = a.app_v + (size_t)kh * 256u;
+        it.pos_new = (uint32_t)ldg(a.app_pos);
+    }
     const bool al16 = ((((uintptr_t)it.kc) | ((uintptr_t)it.vc)) & 15u) == 0;
     const uint32_t n_chunks = (it.n + CP - 1u) / CP;
     const uint32_t c0 = s * a.cps;
@@ -928,12 +964,16 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
      * quantised rows to the caches, and any split whose chunk lists the
      * position uses the same bytes in LDS instead of the fetched row */
     float nx[4] = {0.f, 0.f, 0.f, 0.f};
-    const bool step_lane = IS_STEP(MODE) && tid < 128u;
+    const bool step_lane = STEPL && tid < 128u;
     if (step_lane) {
         const float *src = (tid < 64u ? it.knew : it.vnew) + 32u * ((tid >> 3) & 7u) + 4u * (tid & 7u);
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) nx[i] = ldg(src + i);
     }
+    /* the quantised bytes of the new rows (computed once, with the row DMA
+     * in flight; MODE_PSTEP after the key preparation below) */
+    int nq[4] = {0, 0, 0, 0};
+    float nd = 0.f;
     if (MODE == MODE_PSTEP && wave == 0) {
         /* wave 0 holds the K row (lane l: dims 4l .. 4l+3): RMSNorm + RoPE
          * at the token's position, through LDS in the shared prep layout */
@@ -978,6 +1018,8 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
      * those too */
     asm volatile("" ::: "memory");
     if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
+    /* with the Q and index loads in flight */
+    if (step_lane) nd = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], nq);
     if (MODE == MODE_PSTEP && s == 0u && it.gate) {
         /* the gate halves of the [q | gate] rows go to the gate buffer the
          * merge reads */
@@ -1034,10 +1076,10 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         /* the first chunk's rows, then the second chunk's indices */
         if (q_own && MODE == MODE_DENSE) {
             __builtin_amdgcn_s_waitcnt(0);
-            build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+            build_qa(qraw, g, gqa, jg, nsel, qa, qbias, a.scale_log2, s_qm);
         }
         issue_rows(c0, 0u);
-        if (q_own && MODE != MODE_DENSE) build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+        if (q_own && MODE != MODE_DENSE) build_qa(qraw, g, gqa, jg, nsel, qa, qbias, a.scale_log2, s_qm);
         if (c0 + 1u < c1) {
 #pragma unroll
             for (uint32_t u = 0; u <= NLD; u++) jcur[u] += CP;
@@ -1053,7 +1095,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             if (q_own && c == c0) {
                 /* dense items load no indices: wait for the Q DMAs explicitly */
                 if (MODE == MODE_DENSE) __builtin_amdgcn_s_waitcnt(0);
-                build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+                build_qa(qraw, g, gqa, jg, nsel, qa, qbias, a.scale_log2, s_qm);
             }
         }
         uint8_t *const kraw = rowbuf[bs], *const vraw = rowbuf[bs] + CP * ROWB;
@@ -1061,16 +1103,27 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         TRACE(2);
         /* this chunk's rows (with DB, also the next chunk's indices) have landed */
         __builtin_amdgcn_s_waitcnt(0);
-        if (IS_STEP(MODE)) {
-            /* rows at the appended position take the new token's bytes */
-            const bool mine = tid < CP && pidx[NLD] >= 0 && (uint32_t)pidx[NLD] == it.pos_new;
-            if (__syncthreads_or(mine)) {
-                if (tid < 128u) {
-                    int q[4];
-                    const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
+        if (STEPL) {
+            /* rows at the appended position take the new token's bytes:
+             * wave 0 (thread r owns row r) ballots the matching rows, the
+             * mask goes through LDS with the barrier, and the 128 step lanes
+             * store their precomputed bytes into just those rows */
+            if (wave == 0) {
+                const bool mine = pidx[NLD] >= 0 && (uint32_t)pidx[NLD] == it.pos_new;
+                const uint64_t mm = __ballot(mine);
+                if (lane == 0) {
+                    s_subst[0] = (uint32_t)mm;
+                    s_subst[1] = (uint32_t)(mm >> 32);
+                }
+            }
+            __syncthreads();
+            uint64_t mm = (uint64_t)s_subst[0] | ((uint64_t)s_subst[1] << 32);
+            if (mm) {
+                if (step_lane) {
                     uint8_t *base = (tid < 64u ? kraw : vraw) + 34u * ((tid >> 3) & 7u);
-                    for (uint32_t r = 0; r < CP; r++)
-                        if ((uint32_t)spos[r] == it.pos_new) q8_lane_store(base + r * ROWB, tid & 7u, d, q);
+                    for (; mm; mm &= mm - 1u)
+                        q8_lane_store(base + (uint32_t)__builtin_ctzll(mm) * ROWB, tid & 7u, nd,
+                                      nq);
                 }
                 __syncthreads();
             }
@@ -1086,7 +1139,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
                                   (int32_t)it.pos_new, a.rope_base, a.eps, lane);
                 __syncthreads();
             }
-            build_qa(qraw, g, gqa, jg, nsel, qa, qbias);
+            build_qa(qraw, g, gqa, jg, nsel, qa, qbias, a.scale_log2, s_qm);
             if (DB) __syncthreads(); /* buffer 1 (the Q rows) is refilled below */
         }
         if (c + 1u < c1) {
@@ -1143,7 +1196,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
         float T[4], cm[4];
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
-            const float t = pair32_sum(S[i]) * a.scale_log2;
+            const float t = pair32_sum(S[i]) * s_qm[(4u * jg + i) & 7u];
             T[i] = valid ? t : -INFINITY;
             cm[i] = T[i];
         }
@@ -1312,11 +1365,10 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     /* MODE_STEP: split 0 writes the quantised rows last, so no wait inside
      * the kernel covers these stores (the chunks that list the position
      * took the same bytes in LDS) */
-    if (IS_STEP(MODE) && s == 0u && it.pos_new < it.max_kv && tid < 128u) {
-        int q[4];
-        const float d = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], q);
+    const bool writer = s == 0u && (!APP || item < a.n_kvh);
+    if (STEPL && writer && (APP || it.pos_new < it.max_kv) && step_lane) {
         uint8_t *row = (uint8_t *)(tid < 64u ? kbase : vbase) + (size_t)it.pos_new * rstride;
-        q8_lane_store(row + 34u * ((tid >> 3) & 7u), tid & 7u, d, q);
+        q8_lane_store(row + 34u * ((tid >> 3) & 7u), tid & 7u, nd, nq);
     }
     TRACE(12);
 }
@@ -2900,6 +2952,7 @@ extern "C" bool q4kv_prof_begin(int max_launches) {
 }
 
 extern "C" int q4kv_prof_end(double *total_ms) {
+    if (!q4kv_flush()) return -1;
     g_prof_on = 0;
     if (total_ms) *total_ms = 0.0;
     if (!g_prof_n) return 0;
@@ -3311,10 +3364,19 @@ static bool step_fusable(int kind, uint32_t hd, uint32_t gqa) {
     return kind == Q4KV_Q8 && hd == 256u && (gqa <= 8u || slab_takes(gqa, false));
 }
 
+/* The held append this launch can perform (same caches, whole 256-dim q8_0
+ * rows of its KV heads). */
+static bool held_matches(const AttnArgs &a) {
+    const q4kv_held_append &h = q4kv_held;
+    return h.on && h.kind == Q4KV_Q8 && h.kc == a.kc && h.vc == a.vc &&
+           h.n == a.n_kvh * 256u && h.bpt == a.n_kvh * 272u;
+}
+
 template <int KIND, int MODE>
 static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa,
                         const OutProj *op = nullptr, PartBuf pb = lib_part()) {
     if (any_shape(a.hd, gqa)) {
+        if (!q4kv_flush()) return false;
         if constexpr (IS_STEP(MODE)) {
             return false;
         } else {
@@ -3333,6 +3395,21 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap, rows16);
     if (IS_STEP(MODE) && !fast && !pl.slab && !pl.h16 && !pl.f32w) return false; /* the fused append needs these */
     const uint32_t S = pl.S, cps = pl.cps;
+    /* a held append on these caches rides in the chunk kernel's launch (one
+     * launch pass: the split kernel then the merge); any other launch runs
+     * it first */
+    bool app = false;
+    if constexpr (KIND == Q4KV_Q8 && (MODE == MODE_INDEXED || MODE == MODE_DENSE)) {
+        app = fast && !pl.slab && cps < db_min_chunks() && n_items <= Q4KV_MAX_GRID_Y &&
+              held_matches(a);
+        if (app) {
+            a.app_k = q4kv_held.k;
+            a.app_v = q4kv_held.v;
+            a.app_pos = q4kv_pos_d;
+            q4kv_held.on = 0;
+        }
+    }
+    if (!app && !q4kv_flush()) return false;
     a.S = S;
     a.cps = cps;
     a.part = pb.ptr;
@@ -3385,7 +3462,10 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
             qsa_slab_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (fast && cps >= db_min_chunks())
             qsa_q8d256_k<MODE, true><<<grid, 256, 0, q4kv_stream>>>(a);
-        else if (fast)
+        else if (fast && app) {
+            if constexpr (MODE == MODE_INDEXED || MODE == MODE_DENSE)
+                qsa_q8d256_k<MODE, false, true><<<grid, 256, 0, q4kv_stream>>>(a);
+        } else if (fast)
             qsa_q8d256_k<MODE, false><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (IS_STEP(MODE))
             return false;
@@ -3505,6 +3585,7 @@ extern "C" bool q4_hip_qsa_decode(const float *d_q, const void *d_kcache, const 
 extern "C" bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n_seq,
                                         uint32_t n_head, uint32_t n_kvh, uint32_t hd,
                                         float scale, int kv_f16, uint32_t max_n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
         return false;
     (void)hipGetLastError();
@@ -3539,6 +3620,7 @@ static bool step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32_t n
 extern "C" bool q4_hip_qsa_step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq,
                                       uint32_t n_head, uint32_t n_kvh, uint32_t hd, float scale,
                                       int kv_f16, uint32_t max_n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
         return false;
     return step_batch(d_descs, n_seq, n_head, n_kvh, hd, scale, kv_f16, max_n, lib_part());
@@ -3581,6 +3663,7 @@ extern "C" bool q4kv_scratch_init(void) {
 extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uint32_t n_seq,
                                               uint32_t n_head, uint32_t n_kvh, uint32_t hd,
                                               float scale, int kv_f16, uint32_t max_n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
         return false;
     int dev = -1;
@@ -3633,12 +3716,14 @@ extern "C" int q4kv_trace_read_band(uint64_t *host, size_t n) {
 }
 #endif
 
-extern "C" bool q4_hip_qsa_topk_alloc(void) { return q4kv_ok && q4kv_part != nullptr; }
+extern "C" bool q4_hip_qsa_topk_alloc(void) {
+    Q4KV_FLUSH_OR_FAIL(); return q4kv_ok && q4kv_part != nullptr; }
 
 extern "C" bool q4_hip_qsa_step_prep_batch(const q4kv_prep_step_desc *d_descs, uint32_t n_seq,
                                            uint32_t n_head, uint32_t n_kvh, uint32_t hd,
                                            float scale, int kv_f16, uint32_t max_n,
                                            uint32_t n_rot, float rope_base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_descs || !n_seq || !max_n || !shape_ok(n_head, n_kvh, hd, kv_f16))
         return false;
     const uint32_t gqa = n_head / n_kvh;
@@ -3662,6 +3747,7 @@ extern "C" bool q4_hip_qsa_step_out_batch(const q4kv_step_desc *d_descs,
                                           uint32_t n_head, uint32_t n_kvh, uint32_t hd,
                                           float scale, int kv_f16, uint32_t max_n,
                                           uint32_t n_embd, float y_scale) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_descs || !d_outs || !n_seq || !max_n || !n_embd ||
         !shape_ok(n_head, n_kvh, hd, kv_f16))
         return false;

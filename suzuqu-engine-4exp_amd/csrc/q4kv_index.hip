@@ -967,6 +967,7 @@ bool prep_launch(const float *src, float *dst, float *g, const float *wn, uint32
 extern "C" bool q4_hip_qsa_q_prep_n(const float *d_qg, const float *d_wn, float *d_q,
                                     float *d_g, uint32_t n_head, uint32_t hd, uint32_t n_rot,
                                     int32_t pos0, float base, float eps, uint32_t n_tok) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_qg || !d_q || !d_g || n_head == 0 || n_tok == 0) return false;
     return prep_launch(d_qg, d_q, d_g, d_wn, n_head, hd, n_rot, pos0, base, eps, n_tok,
                        nullptr, "qsa_q_prep");
@@ -974,11 +975,13 @@ extern "C" bool q4_hip_qsa_q_prep_n(const float *d_qg, const float *d_wn, float 
 extern "C" bool q4_hip_qsa_q_prep(const float *d_qg, const float *d_wn, float *d_q, float *d_g,
                                   uint32_t n_head, uint32_t hd, uint32_t n_rot, int32_t pos,
                                   float base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     return q4_hip_qsa_q_prep_n(d_qg, d_wn, d_q, d_g, n_head, hd, n_rot, pos, base, eps, 1);
 }
 extern "C" bool q4_hip_qsa_q_prep_d(const float *d_qg, const float *d_wn, float *d_q,
                                     float *d_g, uint32_t n_head, uint32_t hd, uint32_t n_rot,
                                     float base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !d_qg || !d_q || !d_g || n_head == 0) return false;
     return prep_launch(d_qg, d_q, d_g, d_wn, n_head, hd, n_rot, 0, base, eps, 1, q4kv_pos_d,
                        "qsa_q_prep_d");
@@ -986,16 +989,19 @@ extern "C" bool q4_hip_qsa_q_prep_d(const float *d_qg, const float *d_wn, float 
 extern "C" bool q4_hip_qsa_k_prep_n(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
                                     uint32_t n_rot, int32_t pos0, float base, float eps,
                                     uint32_t n_tok) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_k || n_kvh == 0 || n_tok == 0) return false;
     return prep_launch(d_k, d_k, nullptr, d_wn, n_kvh, hd, n_rot, pos0, base, eps, n_tok,
                        nullptr, "qsa_k_prep");
 }
 extern "C" bool q4_hip_qsa_k_prep(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
                                   uint32_t n_rot, int32_t pos, float base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     return q4_hip_qsa_k_prep_n(d_k, d_wn, n_kvh, hd, n_rot, pos, base, eps, 1);
 }
 extern "C" bool q4_hip_qsa_k_prep_d(float *d_k, const float *d_wn, uint32_t n_kvh, uint32_t hd,
                                     uint32_t n_rot, float base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !d_k || n_kvh == 0) return false;
     return prep_launch(d_k, d_k, nullptr, d_wn, n_kvh, hd, n_rot, 0, base, eps, 1, q4kv_pos_d,
                        "qsa_k_prep_d");
@@ -1003,6 +1009,7 @@ extern "C" bool q4_hip_qsa_k_prep_d(float *d_k, const float *d_wn, uint32_t n_kv
 
 extern "C" bool q4_hip_f32_to_f16_d(void *dst_base, uint32_t stride_elems, const float *src,
                                     uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !dst_base || !src || !n) return false;
     const uint64_t grid = (n + 255u) / 256u;
     if (grid > 0x7fffffffull) return false;
@@ -1015,6 +1022,7 @@ extern "C" bool q4_hip_f32_to_f16_d(void *dst_base, uint32_t stride_elems, const
 extern "C" bool q4_hip_qsa_pool(const void *raw_f16, float *pool, const float *wn, uint32_t hd,
                                 uint32_t ratio, uint32_t b0, uint32_t b1, uint32_t n_rot,
                                 float rope_base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !raw_f16 || !pool || b1 <= b0 || hd != IDX_HD || ratio == 0 || n_rot > hd)
         return false;
     if (((uintptr_t)raw_f16 & 3u) || ((uintptr_t)pool & 7u)) {
@@ -1030,6 +1038,7 @@ extern "C" bool q4_hip_qsa_pool(const void *raw_f16, float *pool, const float *w
 }
 extern "C" bool q4_hip_qsa_pool_d(const void *raw_f16, float *pool, const float *wn, uint32_t hd,
                                   uint32_t ratio, uint32_t n_rot, float rope_base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !raw_f16 || !pool || hd != IDX_HD || ratio == 0 ||
         n_rot > hd)
         return false;
@@ -1046,6 +1055,7 @@ extern "C" bool q4_hip_qsa_pool_d(const void *raw_f16, float *pool, const float 
 extern "C" bool q4_hip_qsa_score(const float *q, const float *pool, float *score,
                                  uint32_t n_tok, uint32_t n_blocks, uint32_t stride,
                                  uint32_t n_head, uint32_t hd, uint32_t pos0, uint32_t ratio) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q || !pool || !score || n_tok == 0 || hd != IDX_HD || n_head == 0 ||
         n_head > 4)
         return false;
@@ -1073,6 +1083,7 @@ extern "C" bool q4_hip_qsa_score(const float *q, const float *pool, float *score
 extern "C" bool q4_hip_qsa_score_d(const float *q, const float *pool, float *score,
                                    uint32_t stride, uint32_t n_head, uint32_t hd,
                                    uint32_t ratio) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !q || !pool || !score || hd != IDX_HD || n_head == 0 ||
         n_head > 4)
         return false;
@@ -1093,6 +1104,7 @@ extern "C" bool q4_hip_qsa_score_d(const float *q, const float *pool, float *sco
 extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok,
                                 uint32_t n_blocks, uint32_t stride, uint32_t k_blk,
                                 uint32_t ratio, uint32_t pos0, uint32_t width) {
+    Q4KV_FLUSH_OR_FAIL();
     (void)n_blocks; /* rows are bounded by each token's visible blocks */
     if (!q4kv_ok || !score || !sel || n_tok == 0 || k_blk == 0 || k_blk > TK_MAXK ||
         width == 0 || ratio == 0)
@@ -1115,6 +1127,7 @@ extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok
 }
 extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride,
                                   uint32_t k_blk, uint32_t ratio, uint32_t width) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !score || !sel || k_blk == 0 || k_blk > TK_MAXK ||
         width == 0 || ratio == 0)
         return false;
@@ -1135,6 +1148,7 @@ extern "C" bool q4_hip_qsa_index_score_d(void *raw_f16, float *pool, const float
                                          float *score, uint32_t stride, uint32_t n_head,
                                          uint32_t hd, uint32_t ratio, uint32_t n_rot,
                                          float rope_base, float eps) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !raw_f16 || !pool || !k_new || !q || !score ||
         hd != IDX_HD || n_head == 0 || n_head > 4 || ratio == 0 || n_rot > hd)
         return false;
@@ -1157,6 +1171,7 @@ extern "C" bool q4_hip_qsa_index_batch(const q4kv_index_desc *d_descs, uint32_t 
                                        uint32_t max_blocks, uint32_t n_head, uint32_t hd,
                                        uint32_t ratio, uint32_t n_rot, float rope_base, float eps,
                                        uint32_t k_blk, uint32_t width) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_descs || n_items == 0 || n_items > 65535u || max_blocks == 0 ||
         hd != IDX_HD || n_head == 0 || n_head > 4 || ratio == 0 || n_rot > hd || k_blk == 0 ||
         k_blk > TK_MAXK || width == 0)

@@ -21,9 +21,30 @@ extern int32_t *q4kv_pos_d;
 extern float *q4kv_part;
 extern size_t q4kv_part_cap;
 
+/* A held q4_hip_kv_append_d: the append of one token's K/V rows at the
+ * device position, recorded instead of launched. A one-token decode on the
+ * same caches performs it inside its own launch; any other library call
+ * first launches it (q4kv_flush), so every caller of the library sees the
+ * same stream order as if it had been launched at once. */
+struct q4kv_held_append {
+    int on;
+    uint8_t *kc, *vc;
+    const float *k, *v;
+    uint32_t n, bpt;
+    int kind;
+};
+extern q4kv_held_append q4kv_held;
+/* Launch the held append, if any. False if that launch failed. */
+bool q4kv_flush(void);
+#define Q4KV_FLUSH_OR_FAIL()                                                   \
+    do {                                                                       \
+        if (!q4kv_flush()) return false;                                       \
+    } while (0)
+
 /* Resolves the no-allocation entry point's static scratch on the current
  * device (q4kv_attn.hip); q4_hip_init calls it once. */
 extern "C" bool q4kv_scratch_init(void);
+
 
 /* The append half of q4_hip_qsa_step_batch for widths the fused kernel
  * does not cover: d_step_descs is a device array of q4kv_step_desc. */

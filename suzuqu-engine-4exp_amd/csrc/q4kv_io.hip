@@ -110,6 +110,7 @@ static bool retire(q4kv_pipe *p, unsigned i) {
 }
 
 extern "C" q4kv_pipe *q4kv_pipe_open(size_t chunk) {
+    if (!q4kv_flush()) return nullptr;
     if (!q4kv_ok || chunk == 0) return nullptr;
     q4kv_pipe *p = (q4kv_pipe *)calloc(1, sizeof(q4kv_pipe));
     if (!p) return nullptr;
@@ -127,6 +128,7 @@ extern "C" q4kv_pipe *q4kv_pipe_open(size_t chunk) {
 }
 
 extern "C" bool q4kv_pipe_finish(q4kv_pipe *p) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!p) return false;
     bool ok = !p->failed;
     for (unsigned k = 0; k < Q4KV_PIPE_NBUF; k++)
@@ -136,6 +138,7 @@ extern "C" bool q4kv_pipe_finish(q4kv_pipe *p) {
 }
 
 extern "C" void q4kv_pipe_close(q4kv_pipe *p) {
+    (void)q4kv_flush();
     if (!p) return;
     (void)q4kv_pipe_finish(p);
     for (int i = 0; i < Q4KV_PIPE_NBUF; i++) {
@@ -147,6 +150,7 @@ extern "C" void q4kv_pipe_close(q4kv_pipe *p) {
 
 extern "C" bool q4kv_pipe_file_to_dev(q4kv_pipe *p, int fd, uint64_t off, void *dst,
                                       uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!p || fd < 0 || !dst || p->failed) return false;
     uint8_t *d = (uint8_t *)dst;
     for (uint64_t o = 0; o < n; o += p->chunk) {
@@ -168,6 +172,7 @@ extern "C" bool q4kv_pipe_file_to_dev(q4kv_pipe *p, int fd, uint64_t off, void *
 
 extern "C" bool q4kv_pipe_dev_to_file(q4kv_pipe *p, int fd, uint64_t off, const void *src,
                                       uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!p || fd < 0 || !src || p->failed) return false;
     const uint8_t *s = (const uint8_t *)src;
     for (uint64_t o = 0; o < n; o += p->chunk) {

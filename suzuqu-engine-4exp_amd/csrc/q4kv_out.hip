@@ -111,6 +111,7 @@ __global__ __launch_bounds__(256) void gemv_q8_any_k(const uint8_t *w, const flo
 /* q8_0 only (ggml type 8); other types return false. */
 extern "C" bool q4_hip_gemv_dd(uint32_t ggml_type, const uint8_t *d_w, uint64_t nrows,
                                uint64_t ncols, const float *d_x, float *d_y, float scale) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d_w || !d_x || !d_y || nrows == 0 || ncols == 0) return false;
     if (ggml_type != 8u || ncols % 32u || nrows > 0xffffffffull || ncols > 0xffffffffull) {
         Q4KV_ERR("gemv_dd: only q8_0 rows of whole blocks are supported");

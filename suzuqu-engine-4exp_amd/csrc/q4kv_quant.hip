@@ -15,6 +15,7 @@
  */
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
+#include <stdlib.h>
 
 #include "q4kv_internal.h"
 
@@ -178,10 +179,12 @@ bool q4kv_append_steps(const void *d_step_descs, uint32_t n_desc, uint32_t n, ui
 
 extern "C" bool q4_hip_kv_append_batch(const q4kv_append_desc *d_descs, uint32_t n_desc,
                                        uint32_t n, uint32_t bpt, int kind) {
+    Q4KV_FLUSH_OR_FAIL();
     return append_batch(d_descs, false, n_desc, n, bpt, kind);
 }
 
 extern "C" bool q4_hip_f32_to_q8(void *dst_q8, const float *src, uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !dst_q8 || !src || n == 0 || (n % 32u) != 0) return false;
     (void)hipGetLastError();
     const uint64_t nb = n / 32u;
@@ -194,6 +197,7 @@ extern "C" bool q4_hip_f32_to_q8(void *dst_q8, const float *src, uint64_t n) {
 }
 
 extern "C" bool q4_hip_f32_to_f16(void *dst_f16, const float *src, uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !dst_f16 || !src || !n) return false;
     (void)hipGetLastError();
     const uint64_t threads = (n + 3u) / 4u;
@@ -204,12 +208,8 @@ extern "C" bool q4_hip_f32_to_f16(void *dst_f16, const float *src, uint64_t n) {
     return q4kv_launch_ok("f32_to_f16");
 }
 
-extern "C" bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k,
-                                   const float *v, uint32_t n, uint32_t bpt, int kind) {
-    if (!q4kv_ok || !q4kv_pos_d || !kcache || !vcache || !k || !v || !n || !bpt)
-        return false;
-    if (kind < Q4KV_F32 || kind > Q4KV_Q8) return false;
-    if (kind == Q4KV_Q8 && (n % 32u)) return false;
+static bool append_launch(uint8_t *kc, uint8_t *vc, const float *k, const float *v, uint32_t n,
+                          uint32_t bpt, int kind) {
     (void)hipGetLastError();
     uint32_t gx;
     if (kind == Q4KV_Q8)
@@ -217,7 +217,42 @@ extern "C" bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k,
     else
         gx = (n + 255u) / 256u;
     dim3 grid(gx, 2);
-    kv_append_k<<<grid, 256, 0, q4kv_stream>>>(k, v, (uint8_t *)kcache, (uint8_t *)vcache, n,
-                                               bpt, kind, q4kv_pos_d);
+    kv_append_k<<<grid, 256, 0, q4kv_stream>>>(k, v, kc, vc, n, bpt, kind, q4kv_pos_d);
     return q4kv_launch_ok("kv_append");
+}
+
+q4kv_held_append q4kv_held = {};
+
+bool q4kv_flush(void) {
+    if (!q4kv_held.on) return true;
+    q4kv_held.on = 0;
+    return append_launch(q4kv_held.kc, q4kv_held.vc, q4kv_held.k, q4kv_held.v, q4kv_held.n,
+                         q4kv_held.bpt, q4kv_held.kind);
+}
+
+/* Q4KV_HOLD_APPEND=0 launches every append at once (no held append). */
+static bool hold_enabled(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_HOLD_APPEND");
+        v = (e && e[0] == '0') ? 0 : 1;
+    }
+    return v != 0;
+}
+
+/* src/q4_rocm.cu:7962-8012. A q8_0 append of whole 256-dim head rows is held
+ * (q4kv_held) for the next library call: a one-token decode over the same
+ * caches performs it in its own launch, any other call launches it first. */
+extern "C" bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k,
+                                   const float *v, uint32_t n, uint32_t bpt, int kind) {
+    if (!q4kv_ok || !q4kv_pos_d || !kcache || !vcache || !k || !v || !n || !bpt)
+        return false;
+    if (kind < Q4KV_F32 || kind > Q4KV_Q8) return false;
+    if (kind == Q4KV_Q8 && (n % 32u)) return false;
+    Q4KV_FLUSH_OR_FAIL();
+    if (kind == Q4KV_Q8 && n % 256u == 0u && bpt == n / 256u * 272u && hold_enabled()) {
+        q4kv_held = q4kv_held_append{1, (uint8_t *)kcache, (uint8_t *)vcache, k, v, n, bpt, kind};
+        return true;
+    }
+    return append_launch((uint8_t *)kcache, (uint8_t *)vcache, k, v, n, bpt, kind);
 }

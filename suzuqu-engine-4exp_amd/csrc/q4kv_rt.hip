@@ -53,6 +53,27 @@ static bool sync_copy(void *dst, const void *src, size_t n, hipMemcpyKind kind) 
     return hipStreamSynchronize(q4kv_stream) == hipSuccess;
 }
 
+/* Releases whatever q4_hip_init had allocated (every handle may be null). */
+static void release_all(void) {
+    if (q4kv_stream) (void)hipStreamSynchronize(q4kv_stream);
+    if (q4kv_part) (void)hipFree(q4kv_part);
+    if (q4kv_pos_d) (void)hipFree(q4kv_pos_d);
+    if (g_pos_h) (void)hipHostFree(g_pos_h);
+    for (int i = 0; i < POS_SLOTS; i++) {
+        if (g_pos_ev[i]) (void)hipEventDestroy(g_pos_ev[i]);
+        g_pos_ev[i] = nullptr;
+        g_pos_used[i] = 0;
+    }
+    if (g_own_stream) (void)hipStreamDestroy(g_own_stream);
+    g_own_stream = nullptr;
+    q4kv_part = nullptr;
+    q4kv_part_cap = 0;
+    q4kv_pos_d = nullptr;
+    g_pos_h = nullptr;
+    q4kv_stream = nullptr;
+    (void)hipGetLastError();
+}
+
 extern "C" bool q4_hip_init(void) {
     if (q4kv_ok) return true;
     int n = 0;
@@ -61,53 +82,46 @@ extern "C" bool q4_hip_init(void) {
         return false;
     }
     if (hipSetDevice(0) != hipSuccess) return false;
-    if (hipStreamCreateWithFlags(&q4kv_stream, hipStreamNonBlocking) != hipSuccess) {
-        (void)hipGetLastError();
-        return false;
-    }
-    g_own_stream = q4kv_stream;
-    if (hipMalloc((void **)&q4kv_pos_d, sizeof(int32_t)) != hipSuccess ||
-        hipHostMalloc((void **)&g_pos_h, POS_SLOTS * sizeof(int32_t), hipHostMallocDefault) !=
-            hipSuccess) {
-        (void)hipGetLastError();
-        return false;
-    }
-    for (int i = 0; i < POS_SLOTS; i++) {
-        if (hipEventCreateWithFlags(&g_pos_ev[i], hipEventDisableTiming) != hipSuccess)
-            return false;
+    /* on any failure below, everything allocated so far is released, so a
+     * later retry starts clean */
+    bool ok = hipStreamCreateWithFlags(&q4kv_stream, hipStreamNonBlocking) == hipSuccess;
+    if (ok) g_own_stream = q4kv_stream;
+    else q4kv_stream = nullptr;
+    ok = ok && hipMalloc((void **)&q4kv_pos_d, sizeof(int32_t)) == hipSuccess;
+    ok = ok && hipHostMalloc((void **)&g_pos_h, POS_SLOTS * sizeof(int32_t),
+                             hipHostMallocDefault) == hipSuccess;
+    for (int i = 0; ok && i < POS_SLOTS; i++) {
+        ok = hipEventCreateWithFlags(&g_pos_ev[i], hipEventDisableTiming) == hipSuccess;
         g_pos_used[i] = 0;
     }
-    *g_pos_h = 0;
-    if (hipMemcpy(q4kv_pos_d, g_pos_h, sizeof(int32_t), hipMemcpyHostToDevice) !=
-        hipSuccess)
-        return false;
-    if (hipMalloc((void **)&q4kv_part, (size_t)Q4KV_PART_FLOATS * sizeof(float)) ==
-        hipSuccess)
-        q4kv_part_cap = Q4KV_PART_FLOATS;
-    else {
-        (void)hipGetLastError();
-        q4kv_part = nullptr;
-        q4kv_part_cap = 0;
+    if (ok) {
+        *g_pos_h = 0;
+        ok = hipMemcpy(q4kv_pos_d, g_pos_h, sizeof(int32_t), hipMemcpyHostToDevice) ==
+             hipSuccess;
     }
-    if (!q4kv_scratch_init()) return false;
+    if (ok) {
+        if (hipMalloc((void **)&q4kv_part, (size_t)Q4KV_PART_FLOATS * sizeof(float)) ==
+            hipSuccess)
+            q4kv_part_cap = Q4KV_PART_FLOATS;
+        else {
+            (void)hipGetLastError();
+            q4kv_part = nullptr;
+            q4kv_part_cap = 0;
+        }
+    }
+    ok = ok && q4kv_scratch_init();
+    if (!ok) {
+        release_all();
+        return false;
+    }
     q4kv_ok = 1;
     return true;
 }
 
 extern "C" void q4_hip_shutdown(void) {
     if (!q4kv_ok) return;
-    (void)hipStreamSynchronize(q4kv_stream);
-    if (q4kv_part) (void)hipFree(q4kv_part);
-    if (q4kv_pos_d) (void)hipFree(q4kv_pos_d);
-    if (g_pos_h) (void)hipHostFree(g_pos_h);
-    for (int i = 0; i < POS_SLOTS; i++) (void)hipEventDestroy(g_pos_ev[i]);
-    (void)hipStreamDestroy(g_own_stream);
-    g_own_stream = nullptr;
-    q4kv_part = nullptr;
-    q4kv_part_cap = 0;
-    q4kv_pos_d = nullptr;
-    g_pos_h = nullptr;
-    q4kv_stream = nullptr;
+    (void)q4kv_flush();
+    release_all();
     q4kv_ok = 0;
 }
 
@@ -117,6 +131,7 @@ extern "C" bool q4_hip_ok(void) { return q4kv_ok != 0; }
  * compute stream, so its producers and these kernels stay ordered); NULL
  * returns to the library's own stream. Not while capturing. */
 extern "C" bool q4kv_use_stream(void *stream) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || q4kv_capturing) return false;
     (void)hipStreamSynchronize(q4kv_stream);
     q4kv_stream = stream ? (hipStream_t)stream : g_own_stream;
@@ -134,45 +149,53 @@ extern "C" void *q4_hip_malloc(size_t n) {
 }
 
 extern "C" void q4_hip_free(void *p) {
+    (void)q4kv_flush();
     if (p) (void)hipFree(p);
 }
 
 extern "C" bool q4_hip_h2d(void *d, const void *h, size_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d || !h || n == 0) return false;
     return sync_copy(d, h, n, hipMemcpyHostToDevice);
 }
 
 extern "C" bool q4_hip_d2h(void *h, const void *d, size_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d || !h || n == 0) return false;
     return sync_copy(h, d, n, hipMemcpyDeviceToHost);
 }
 
 extern "C" bool q4_hip_h2d_async(void *d, const void *h, uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d || !h || !n) return false;
     return hipMemcpyAsync(d, h, (size_t)n, hipMemcpyHostToDevice, q4kv_stream) ==
            hipSuccess;
 }
 
 extern "C" bool q4_hip_d2h_async(void *h, const void *d, uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d || !h || !n) return false;
     return hipMemcpyAsync(h, d, (size_t)n, hipMemcpyDeviceToHost, q4kv_stream) ==
            hipSuccess;
 }
 
-/* f32 KV width store: a device-to-device copy on the compute stream
- * (src/q4_rocm.cu:5667-5670). Asynchronous, like every other KV write. */
+/* f32 KV width store (src/q4_rocm.cu:5667-5670): a device-to-device copy
+ * ordered on the compute stream that returns once it has landed, as the
+ * reference's does; inside a capture it becomes a copy node. */
 extern "C" bool q4_hip_copy(float *d, const float *s, uint64_t n) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !d || !s || !n) return false;
-    return hipMemcpyAsync(d, s, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice,
-                          q4kv_stream) == hipSuccess;
+    return sync_copy(d, s, (size_t)n * sizeof(float), hipMemcpyDeviceToDevice);
 }
 
 extern "C" bool q4_hip_stream_sync(void) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok) return false;
     return hipStreamSynchronize(q4kv_stream) == hipSuccess;
 }
 
 extern "C" void q4_hip_sync(void) {
+    (void)q4kv_flush();
     if (q4kv_ok) (void)hipDeviceSynchronize();
 }
 
@@ -191,11 +214,13 @@ extern "C" void *q4_hip_host_alloc(size_t n) {
 }
 
 extern "C" void q4_hip_host_free(void *p) {
+    (void)q4kv_flush();
     if (p) (void)hipHostFree(p);
 }
 
 /* ---- device decode position (src/q4_rocm.cu:6218-6227) ---- */
 extern "C" void q4_hip_pos_push(int32_t pos) {
+    (void)q4kv_flush();
     if (!q4kv_pos_d || !g_pos_h || !q4kv_stream) return;
     const unsigned i = g_pos_next++ % POS_SLOTS;
     if (g_pos_used[i] && !q4kv_capturing) (void)hipEventSynchronize(g_pos_ev[i]);
@@ -213,6 +238,8 @@ extern "C" int q4_hip_pos_dev_ok(void) { return q4kv_pos_d != nullptr && g_pos_h
 /* ---- graph capture (src/q4_rocm.cu:8162-8245) ---- */
 extern "C" int q4_hip_graph_begin(void) {
     if (!q4kv_ok || q4kv_capturing) return 0;
+    /* an append held before the capture runs eagerly, outside the graph */
+    if (!q4kv_flush()) return 0;
     if (hipStreamBeginCapture(q4kv_stream, hipStreamCaptureModeThreadLocal) !=
         hipSuccess) {
         (void)hipGetLastError();
@@ -224,9 +251,33 @@ extern "C" int q4_hip_graph_begin(void) {
 
 extern "C" void *q4_hip_graph_end(void) {
     if (!q4kv_capturing) return nullptr;
+    /* an append held inside the capture becomes a node of the graph */
+    const bool flushed = q4kv_flush();
     q4kv_capturing = 0;
     hipGraph_t g = nullptr;
-    if (hipStreamEndCapture(q4kv_stream, &g) != hipSuccess || !g) {
+    if (hipStreamEndCapture(q4kv_stream, &g) != hipSuccess || !g || !flushed) {
+        (void)hipGetLastError();
+        if (g) (void)hipGraphDestroy(g);
+        /* A failed end can leave the stream in capture state, which fails
+         * every later launch on it (the engine then re-runs the step
+         * eagerly: src/q4_fwd.c:1336-1347). Replace such a stream: the
+         * library's own is recreated; an adopted caller stream is dropped
+         * for a new library stream. */
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(q4kv_stream, &cs) == hipSuccess &&
+            cs != hipStreamCaptureStatusNone) {
+            hipStream_t ns = nullptr;
+            if (q4kv_stream == g_own_stream) (void)hipStreamDestroy(g_own_stream);
+            g_own_stream = nullptr;
+            if (hipStreamCreateWithFlags(&ns, hipStreamNonBlocking) == hipSuccess) {
+                g_own_stream = q4kv_stream = ns;
+                Q4KV_ERR("graph end: the stream was left capturing; replaced it");
+            } else {
+                q4kv_stream = nullptr;
+                q4kv_ok = 0;
+                Q4KV_ERR("graph end: the stream was left capturing and no new one could be made");
+            }
+        }
         (void)hipGetLastError();
         return nullptr;
     }
@@ -250,11 +301,13 @@ extern "C" uint32_t q4_hip_graph_nodes(void *exec) {
 }
 
 extern "C" bool q4_hip_graph_launch(void *exec) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!exec) return false;
     return hipGraphLaunch((hipGraphExec_t)exec, q4kv_stream) == hipSuccess;
 }
 
 extern "C" void q4_hip_graph_free(void *exec) {
+    (void)q4kv_flush();
     if (exec) (void)hipGraphExecDestroy((hipGraphExec_t)exec);
 }
 
@@ -264,6 +317,7 @@ static hipEvent_t g_ev0[Q4KV_TIMERS], g_ev1[Q4KV_TIMERS];
 static int g_ev_made[Q4KV_TIMERS];
 
 extern "C" bool q4kv_timer_begin(int slot) {
+    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || slot < 0 || slot >= Q4KV_TIMERS) return false;
     if (!g_ev_made[slot]) {
         if (hipEventCreate(&g_ev0[slot]) != hipSuccess ||
@@ -275,6 +329,7 @@ extern "C" bool q4kv_timer_begin(int slot) {
 }
 
 extern "C" double q4kv_timer_end_ms(int slot) {
+    if (!q4kv_flush()) return -1;
     if (!q4kv_ok || slot < 0 || slot >= Q4KV_TIMERS || !g_ev_made[slot]) return -1.0;
     if (hipEventRecord(g_ev1[slot], q4kv_stream) != hipSuccess) return -1.0;
     if (hipEventSynchronize(g_ev1[slot]) != hipSuccess) return -1.0;
