@@ -77,11 +77,13 @@ bool q4_hip_kv_append_d(void *kcache, void *vcache, const float *k, const float 
  * Shapes, as the reference accepts them: head_dim 1..256 (a multiple of 32
  * for q8_0, whose rows are 32-element blocks), n_head a multiple of n_kvh,
  * any number of query heads per KV head.
- * Value range: the MFMA kernels carry q (some of them q * scale / ln 2) as
- * fp16 parts, so query values must stay below 65504 in magnitude; the
- * prefill band kernel (q8_0, head_dim 256, prefill-sized indexed calls)
- * dequantises K and V to fp16 parts like the reference's prefill tile, so
- * cache values must too there. */
+ * Value range: any finite query. The MFMA kernels divide each head's q
+ * (some of them q * scale / ln 2) by the power of two that brings its
+ * largest magnitude into [0.5, 1) before splitting it into fp16 parts, and
+ * multiply the head's scores back (exact). The prefill band kernel (q8_0,
+ * head_dim 256, prefill-sized indexed calls) dequantises K and V to fp16
+ * parts like the reference's prefill tile, so cache values must stay below
+ * 65504 in magnitude there. */
 /* Dense causal attention: token t of n_tok attends positions
  * 0 .. min(kv_base+t+1, max_kv)-1. q/gate/out are [n_tok][n_head][hd] fp32;
  * out = softmax(q.k*scale) @ v * sigmoid(gate) (src/q4.h:906-909). */

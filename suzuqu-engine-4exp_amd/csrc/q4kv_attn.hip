@@ -455,6 +455,8 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float vsc[KIND == Q4KV_Q8 ? 8u * CP : 4u];
     __shared__ int32_t s_pos[CP];
     __shared__ float s_cmax[NQW][NH], s_psum[NQW][NH];
+    /* per head: scale_log2 x 2^e, e the power of two its q was divided by */
+    __shared__ float s_qm[NH];
 
     TRACE(0);
     uint32_t s, item;
@@ -585,9 +587,25 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
 #pragma unroll
             for (uint32_t hg = 0; hg < HG; hg++) {
                 const uint32_t g = hg * 8u + (mrow & 7u);
+                /* q divided by the power of two 2^e that brings the head's
+                 * largest |q| into [0.5, 1) (exact): its fp16 parts never
+                 * overflow; the scores are multiplied by scale_log2 x 2^e.
+                 * The head's lanes: rows g, g + 8, k-groups 0-3. */
+                float am = 0.f;
+#pragma unroll
+                for (uint32_t b = 0; b < NB; b++)
+#pragma unroll
+                    for (uint32_t k = 0; k < 4u; k++)
+                        am = fmaxf(am, fmaxf(fabsf(qv[hg][b][k][0]), fabsf(qv[hg][b][k][1])));
+                am = fmaxf(am, __shfl_xor(am, 8));
+                am = fmaxf(am, __shfl_xor(am, 16));
+                am = fmaxf(am, __shfl_xor(am, 32));
+                const int e = (am > 0.f && am <= 3.4e38f) ? __builtin_amdgcn_frexp_expf(am) : 0;
+                const float qf = __builtin_ldexpf(1.f, -e);
+                if (jg == 0u && mrow < 8u) s_qm[g] = __builtin_ldexpf(a.scale_log2, e);
 #pragma unroll
                 for (uint32_t b = 0; b < 8u; b++) {
-                    const float qscale = (g < gqa && b < NB) ? 1.f : 0.f;
+                    const float qscale = (g < gqa && b < NB) ? qf : 0.f;
 #pragma unroll
                     for (uint32_t k = 0; k < 4u; k++) {
                         qa[hg][b][2u * k] = split_hl(qv[hg][b][k][0] * qscale, lo_row);
@@ -662,7 +680,7 @@ __global__ __launch_bounds__(256) void qsa_attn_k(AttnArgs a) {
 #pragma unroll
                 for (uint32_t i = 0; i < 4u; i++) {
                     const float tot = S[hg][i] + xor32(S[hg][i]);
-                    T[hg][i] = valid ? tot * a.scale_log2 : -INFINITY;
+                    T[hg][i] = valid ? tot * s_qm[hg * 8u + ((4u * jg + i) & 7u)] : -INFINITY;
                     const float cm = row16_max(T[hg][i]);
                     if (mrow == 0 && jg < 2u) s_cmax[wave][hg * 8u + 4u * jg + i] = cm;
                 }
@@ -1473,6 +1491,8 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t vsT[NSLAB][8][SLAB];
     __shared__ __attribute__((aligned(16))) int32_t s_pos[NE];
     __shared__ float s_m[4][8], s_l[4][8];
+    /* per head: the power of two 2^e its q was divided by (scores x 2^e) */
+    __shared__ float s_qm[8 * HG];
     /* MODE_PSTEP: the prepared query rows and the prepared new key row */
     constexpr bool PREP = MODE == MODE_PSTEP;
     __shared__ __attribute__((aligned(16))) float qst[PREP ? 8u * HG : 1u][PREP ? 256u : 1u];
@@ -1601,7 +1621,25 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         for (uint32_t i = 0; i < 4u; i++) nk[i] = kst[off + i];
     }
 
-    /* ---- Q^T operands, built once per workgroup ---- */
+    /* ---- Q^T operands, built once per workgroup ----
+     * Each head's q (scale folded in) is first divided by the power of two
+     * 2^e that brings its largest magnitude into [0.5, 1) (exact), so its
+     * fp16 parts neither overflow nor lose relative precision at any
+     * magnitude of q; the head's scores are multiplied back by 2^e. The 32
+     * threads of a head slot are lanes 32 (t_hh mod 2) .. + 31 of one wave. */
+#pragma unroll
+    for (uint32_t k = 0; k < HG; k++) {
+        float am = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; i++) am = fmaxf(am, fabsf(qx[k][i]));
+#pragma unroll
+        for (uint32_t o = 1; o < 32u; o <<= 1) am = fmaxf(am, __shfl_xor(am, (int)o));
+        const int e = (am > 0.f && am <= 3.4e38f) ? __builtin_amdgcn_frexp_expf(am) : 0;
+        const float f = __builtin_ldexpf(1.f, -e);
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; i++) qx[k][i] *= f;
+        if ((tid & 31u) == 0u) s_qm[8u * k + t_hh] = __builtin_ldexpf(1.f, e);
+    }
 #pragma unroll
     for (uint32_t k = 0; k < HG; k++) {
         uint32_t hw[4], lw[4];
@@ -1622,6 +1660,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     for (uint32_t t = 0; t < 16u; t++) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
     const h8_t neg = (h8_t)((_Float16)-1152.0f);
     const uint16_t *const qBw = &qB[hg][0][jg][c][0];
+    const float qmul = s_qm[8u * hg + (c & 7u)]; /* this lane's column's head */
     const h8_t k_bias = (h8_t)((_Float16)1152.0f);
 
     for (uint32_t pass = 0; pass < n_pass; pass++) {
@@ -1706,8 +1745,8 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             float T[8];
 #pragma unroll
             for (uint32_t i = 0; i < 4u; i++) {
-                T[i] = add_ror8(S[0][i]);
-                T[4u + i] = add_ror8(S[1][i]);
+                T[i] = add_ror8(S[0][i]) * qmul;
+                T[4u + i] = add_ror8(S[1][i]) * qmul;
             }
             float mx = fmax3v(fmax3v(T[0], T[1], T[2]), fmax3v(T[3], T[4], T[5]), fmax2(T[6], T[7]));
             mx = max32(max16(mx));
@@ -1919,6 +1958,8 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
     /* Q^T operands [head group][block][k-group][column][8 fp16] */
     __shared__ __attribute__((aligned(16))) uint16_t qB[HG][8][4][16][8];
     __shared__ float s_m[4][8], s_l[4][8];
+    /* per head: the power of two 2^e its q was divided by (scores x 2^e) */
+    __shared__ float s_qm[8 * HG];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t slab = wave / HG, hg = wave % HG;
@@ -2002,7 +2043,25 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
     int32_t pos = -1;
     bool any = n_pass > 0u ? issue(0u, pos) : false;
 
-    /* ---- Q^T operands, built once per workgroup ---- */
+    /* ---- Q^T operands, built once per workgroup ----
+     * Each head's q (scale folded in) is first divided by the power of two
+     * 2^e that brings its largest magnitude into [0.5, 1) (exact), so its
+     * fp16 parts neither overflow nor lose relative precision at any
+     * magnitude of q; the head's scores are multiplied back by 2^e. The 32
+     * threads of a head slot are lanes 32 (t_hh mod 2) .. + 31 of one wave. */
+#pragma unroll
+    for (uint32_t k = 0; k < HG; k++) {
+        float am = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; i++) am = fmaxf(am, fabsf(qx[k][i]));
+#pragma unroll
+        for (uint32_t o = 1; o < 32u; o <<= 1) am = fmaxf(am, __shfl_xor(am, (int)o));
+        const int e = (am > 0.f && am <= 3.4e38f) ? __builtin_amdgcn_frexp_expf(am) : 0;
+        const float f = __builtin_ldexpf(1.f, -e);
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; i++) qx[k][i] *= f;
+        if ((tid & 31u) == 0u) s_qm[8u * k + t_hh] = __builtin_ldexpf(1.f, e);
+    }
 #pragma unroll
     for (uint32_t k = 0; k < HG; k++) {
         uint32_t hw[4], lw[4];
@@ -2021,6 +2080,7 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
 #pragma unroll
     for (uint32_t t = 0; t < 16u; t++) acc[t] = (f4_t){0.f, 0.f, 0.f, 0.f};
     const uint16_t *const qBw = &qB[hg][0][jg][c][0];
+    const float qmul = s_qm[8u * hg + (c & 7u)]; /* this lane's column's head */
 
     for (uint32_t pass = 0; pass < n_pass; pass++) {
         if (pass > 0u) any = issue(pass, pos);
@@ -2069,7 +2129,7 @@ __global__ __launch_bounds__(256, 2) void qsa_h16_k(AttnArgs a) {
             float T[4];
 #pragma unroll
             for (uint32_t i = 0; i < 4u; i++) {
-                const float x = add_ror8(S[i]);
+                const float x = add_ror8(S[i]) * qmul;
                 T[i] = (vmask >> (4u * jg + i)) & 1u ? x : -INFINITY;
             }
             float mx = fmax2(fmax2(T[0], T[1]), fmax2(T[2], T[3]));
@@ -2558,14 +2618,34 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
     TRACEB(1);
     const uint32_t n_pass = (uint32_t)(hi - lo) / BP + 1u;
 
-    /* the Q^T operands of this wave's tokens, natural dim order */
+    /* the Q^T operands of this wave's tokens, natural dim order. Each head's
+     * q x scale is divided by the power of two 2^e that brings its largest
+     * magnitude into [0.5, 1) (exact: the fp16 parts neither overflow nor
+     * lose relative precision), and its scores are multiplied by qmul = 2^e;
+     * the eight lanes holding a head (columns c, c + 8, k-groups 0-3) find
+     * its maximum together. */
     h8_t qB[TW][8];
+    float qmul[TW];
 #pragma unroll
     for (uint32_t k = 0; k < TW; k++) {
         const uint32_t t = t0 + k, h = c & 7u;
         const bool hv = t < n_tok && h < gqa;
-        const float qs = hv ? a.scale_log2 : 0.f;
         const float *qr = a.q + ((size_t)(t < n_tok ? t : 0u) * a.n_head + kh * gqa + (hv ? h : 0u)) * 256u;
+        float am = 0.f;
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++) {
+            const f4_t x0 = ldg((const f4_t *)(qr + 32u * b + 8u * jg));
+            const f4_t x1 = ldg((const f4_t *)(qr + 32u * b + 8u * jg + 4u));
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) am = fmaxf(am, fmaxf(fabsf(x0[i]), fabsf(x1[i])));
+        }
+        am = fmaxf(am, __shfl_xor(am, 8));
+        am = fmaxf(am, __shfl_xor(am, 16));
+        am = fmaxf(am, __shfl_xor(am, 32));
+        am *= a.scale_log2;
+        const int e = (am > 0.f && am <= 3.4e38f) ? __builtin_amdgcn_frexp_expf(am) : 0;
+        qmul[k] = __builtin_ldexpf(1.f, e);
+        const float qs = hv ? __builtin_ldexpf(a.scale_log2, -e) : 0.f;
 #pragma unroll
         for (uint32_t b = 0; b < 8u; b++) {
             const f4_t x0 = ldg((const f4_t *)(qr + 32u * b + 8u * jg));
@@ -2716,7 +2796,7 @@ __global__ __launch_bounds__(512, 2) void qsa_band_k(AttnArgs a) {
 #pragma unroll
             for (uint32_t i = 0; i < 8u; i++) {
                 const int32_t P = base + (int32_t)((i < 4u ? 0u : 16u) + 4u * jg + (i & 3u));
-                const float x = add_ror8(S[k][i >> 2][i & 3u]);
+                const float x = add_ror8(S[k][i >> 2][i & 3u]) * qmul[k];
                 T[i] = (P >= ps[k] && P <= pe[k]) ? x : -INFINITY;
             }
             float mx = fmax3v(fmax3v(T[0], T[1], T[2]), fmax3v(T[3], T[4], T[5]), fmax2(T[6], T[7]));

@@ -1,9 +1,12 @@
-"""Values of large magnitude on the head_dim-256 q8_0 kernels (chunk,
-slab, band), against the oracle (|got - ref| <= 2e-3 + 1e-3*|ref|).
+"""Values of large and small magnitude on the MFMA kernels, against the
+oracle (|got - ref| <= 2e-3 + 1e-3*|ref|).
 
-The kernels carry Q as fp16 hi/lo parts, so |q| (times the softmax scale
-where a kernel folds it in) must stay inside fp16's range; within that
-range the results must not depend on the magnitude. Here one 32-dimension
+The kernels carry Q as fp16 hi/lo parts after dividing each head's q (times
+the softmax scale where a kernel folds it in) by the power of two that
+brings its largest magnitude into [0.5, 1), so no range of q is excluded
+and the results must not depend on the magnitude:
+test_query_magnitude_any runs queries x 1e5 and x 1e-4 through every MFMA
+kernel (chunk, slab, band, f16, f32, generic). Here one 32-dimension
 block of every head sums to about +704 and another to about -640 (about +63
 and -58 after the scale): a kernel that folded the +1152 bias of its
 int8 -> fp16 K operands into a product with those sums (-1152 x 63 is
@@ -83,5 +86,42 @@ def test_large_v_values(rt, oracle, n_head, n_tok):
     want = oracle.attn(q[ts], kb, vb, 2, n_head, n_kvh, hd, len(ts), idx=sel[ts].ravel(),
                        width=width, tok_stride=n_kvh * width, kvh_stride=width, max_kv=ctx,
                        threads=8)
+    # the unit-scale bar (2e-3 absolute) scaled by the data's factor 1000:
+    # the outputs are 1000x the unit-scale ones, and so are their errors
     assert_attn_close(got[ts], want, atol=2.0, rtol=1e-3,
                       what=f"large v values n_head={n_head} n_tok={n_tok}")
+
+
+# (kind, head_dim, query heads, tokens): the chunk kernel (q8, 8 per KV
+# head), the slab kernel (16), the band + slab prefill kernels, the f16
+# kernel (8 and 16), the f32 kernel, the generic MFMA kernel (q8, hd 128)
+@pytest.mark.parametrize("kind,hd,n_head,n_tok", [(2, 256, 16, 1), (2, 256, 32, 1),
+                                                  (2, 256, 16, 300), (1, 256, 16, 1),
+                                                  (1, 256, 32, 1), (0, 256, 16, 1),
+                                                  (2, 128, 16, 1)])
+@pytest.mark.parametrize("qscale", [1e5, 1e-4])
+def test_query_magnitude_any(rt, oracle, kind, hd, n_head, n_tok, qscale):
+    """Queries x 1e5 (|q| up to ~4e6, far past fp16's 65504; the softmax is
+    then nearly one-hot) and x 1e-4 (nearly uniform weights) against the fp64
+    oracle on the same cache bytes, at the unscaled bar."""
+    n_kvh, width = 2, 2051
+    note(f"query magnitude kind={kind} hd={hd} n_head={n_head} n_tok={n_tok} x{qscale:g}")
+    rng = np.random.default_rng(9500 + 7 * kind + hd + n_head + n_tok + int(qscale > 1))
+    base = 6000
+    ctx = base + n_tok
+    k, v = heads(rng, (ctx, n_kvh), hd=hd), heads(rng, (ctx, n_kvh), hd=hd)
+    q = heads(rng, (n_tok, n_head), hd=hd) * np.float32(qscale)
+    kc, _ = quantize_on_gpu(rt, k, kind)
+    vc, _ = quantize_on_gpu(rt, v, kind)
+    sel = np.stack([np.stack([selection(rng, base + t) for _ in range(n_kvh)])
+                    for t in range(n_tok)]).astype(np.int32)
+    got = gpu_idx_kv(rt, q, kc, vc, kind, n_head, n_kvh, hd, sel.ravel(), width,
+                     n_kvh * width, width, ctx)
+    rt.free(kc)
+    rt.free(vc)
+    ts = np.arange(n_tok) if n_tok <= 8 else np.unique(
+        np.concatenate([[0, n_tok - 1], rng.choice(n_tok, 40, replace=False)]))
+    want = oracle.attn(q[ts], oracle.encode(k, kind), oracle.encode(v, kind), kind, n_head,
+                       n_kvh, hd, len(ts), idx=sel[ts].ravel(), width=width,
+                       tok_stride=n_kvh * width, kvh_stride=width, max_kv=ctx, threads=8)
+    assert_attn_close(got[ts], want, what=f"query x{qscale:g} kind {kind} hd {hd}")
