@@ -53,7 +53,13 @@ def test_large_query_blocks(rt, oracle, n_head, n_tok):
     want = oracle.attn(q[ts], kb, vb, 2, n_head, n_kvh, hd, len(ts), idx=sel[ts].ravel(),
                        width=width, tok_stride=n_kvh * width, kvh_stride=width, max_kv=ctx,
                        threads=8)
-    assert_attn_close(got[ts], want, what=f"large query blocks n_head={n_head} n_tok={n_tok}")
+    # Outputs here reach |ref| ~ 25 (the softmax concentrates on positions
+    # whose outlier V channels are large), and the scores ~1e3: fp32 rounding
+    # of those scores alone moves such outputs by ~1e-4 relative (~2.5e-3
+    # absolute), so an fp32 reference would miss a 2e-3 max-abs bar against
+    # this fp64 oracle too. The bar is the allclose form 2e-3 + 1e-3 |ref|.
+    assert_attn_close(got[ts], want, what=f"large query blocks n_head={n_head} n_tok={n_tok}",
+                      combined=True)
 
 
 @pytest.mark.parametrize("n_head,n_tok", [(16, 1), (32, 1), (16, 700), (32, 300)])
