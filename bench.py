@@ -356,6 +356,25 @@ def _time_direct(b, enqueue, n_sets, steps):
 
 
 USE_GRAPHS = True  # --graphs 0: direct launches only (profiling runs)
+CPU_BUDGET = 3.0   # seconds of CPU baseline per extra configuration (0: none)
+
+
+def _cpu_rate(fn, budget):
+    """Seconds per call of fn on this host, from calls repeated for about
+    `budget` seconds (at least twice)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget and n >= 2:
+            return el / n
+
+
+def _oracle():
+    from oracle_ffi import Oracle
+    return Oracle()
 
 
 def _time_both(b, enqueue, n_sets, steps):
@@ -436,12 +455,43 @@ def config2(b, steps=200, sets=10):
     t, t_graph = _time_both(b, lambda r: lib.q4_hip_qsa_step_batch(
         dd + r * n_seq * sz, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH), sets, steps)
     byts = n_seq * LAYER_B
+    cpu = None
+    if CPU_BUDGET > 0:
+        # the oracle's fp32 path (1 thread) on 4 of the 32 sequences (their
+        # caches read back), each an append + attention; the step's time is
+        # the sample's mean per sequence x 32 (the work per sequence does not
+        # depend on its context length)
+        orc = _oracle()
+        sample = [0, 9, 18, 27]
+        per = []
+        for s_ in sample:
+            kc, vc, L = caches[s_]
+            hk, hv = rt.download(kc, L * BPT), rt.download(vc, L * BPT)
+            q = rt.download(dq + s_ * QO_B, QO_B, np.float32).reshape(1, N_HEAD, HD)
+            row = s_ * N_KVH * HD * 4
+            nk = rt.download(dnk + row, N_KVH * HD * 4, np.float32)
+            nv = rt.download(dnv + row, N_KVH * HD * 4, np.float32)
+            idx = sel[0, s_].ravel()
+
+            def one():
+                orc.lib.orc_kv_append(hk.ctypes.data, hv.ctypes.data, nk.ctypes.data,
+                                      nv.ctypes.data, N_KVH * HD, BPT, 2, L - 1)
+                orc.attn(q, hk, hv, 2, N_HEAD, N_KVH, HD, 1, idx=idx, width=WIDTH,
+                         tok_stride=N_KVH * WIDTH, kvh_stride=WIDTH, max_kv=L, scale=1.0 / 16,
+                         dbl=False, threads=1)
+            per.append(_cpu_rate(one, CPU_BUDGET / len(sample)))
+        t_cpu = float(np.mean(per)) * n_seq
+        cpu = {"us_per_step": round(t_cpu * 1e6, 1), "gbs": round(byts / t_cpu / 1e9, 4),
+               "cores": 1, "kind": "port",
+               "sample": f"sequences {sample} (append + attention each, fp32 C restatement, "
+                         f"1 thread); extrapolated x32 to the step"}
     for kc, vc, _ in caches:
         rt.free(kc)
         rt.free(vc)
     for p_ in (dq, dnk, dnv, dout, dsel, dd):
         rt.free(p_)
-    return {"what": "32 sequences (ctx log-uniform 8192-131072, seed 1236), one batched decode "
+    return {"cpu_baseline": cpu,
+            "what": "32 sequences (ctx log-uniform 8192-131072, seed 1236), one batched decode "
                     "step each: q8_0 append + sparse attention over 2x2051 positions",
             "us_per_step": round(t * 1e6, 2), "graph_us_per_step": _us(t_graph),
             "bytes_per_step": byts,
@@ -494,9 +544,36 @@ def config3(b, reps=4):
     rt.sync()
     wall = (time.perf_counter() - t0) / reps
     flop = chunk * N_HEAD * WIDTH * HD * 4
+    cpu = None
+    if CPU_BUDGET > 0:
+        # the oracle (fp32 path, 1 thread): the chunk's q8_0 quantisation
+        # timed whole, the attention on 32 sampled queries; the layer's time is
+        # quantisation + per-query time x 8192
+        orc = _oracle()
+        hk, hv = rt.download(kc, max_kv * BPT), rt.download(vc, max_kv * BPT)
+        xk = rt.download(nk, n * 4, np.float32)
+        xv = rt.download(nv, n * 4, np.float32)
+        ts = np.random.default_rng(7).choice(chunk, 32, replace=False)
+        qs = [rt.download(dq + int(t) * QO_B, QO_B, np.float32).reshape(1, N_HEAD, HD) for t in ts]
+        t_q = _cpu_rate(lambda: (orc.quant_q8(xk), orc.quant_q8(xv)), CPU_BUDGET / 3)
+        k = [0]
+
+        def one():
+            i = k[0] % len(ts)
+            k[0] += 1
+            orc.attn(qs[i], hk, hv, 2, N_HEAD, N_KVH, HD, 1, idx=sel[ts[i]].ravel(), width=WIDTH,
+                     tok_stride=N_KVH * WIDTH, kvh_stride=WIDTH, max_kv=max_kv, scale=1.0 / 16,
+                     dbl=False, threads=1)
+        t_a = _cpu_rate(one, 2 * CPU_BUDGET / 3)
+        t_cpu = t_q + t_a * chunk
+        cpu = {"us_per_layer": round(t_cpu * 1e6, 1), "tflops": round(flop / t_cpu / 1e12, 5),
+               "cores": 1, "kind": "port",
+               "sample": "q8_0 quantisation of the whole chunk + attention of 32 sampled "
+                         "queries (fp32 C restatement, 1 thread), extrapolated to 8192 queries"}
     for p_ in (kc, vc, nk, nv, dq, dout, dsel):
         rt.free(p_)
-    return {"what": "8192-token q8_0 chunk appended to a 16384-token cache, then 8192 "
+    return {"cpu_baseline": cpu,
+            "what": "8192-token q8_0 chunk appended to a 16384-token cache, then 8192 "
                     "queries x 16 heads over per-KV-head lists of 2051 (3 sinks + 512 recent "
                     "+ 1536 distinct uniform earlier positions)",
             "us_per_layer": round(wall * 1e6, 1), "gflop": round(flop / 1e9, 1),
@@ -537,6 +614,28 @@ def config4(b, steps=100, sets=16, layers=12):
                      "bytes_per_layer": byts,
                      "gbs": round(byts * layers / t / 1e9, 1), "layers_per_step": layers,
                      "selection_sets": sets, "gathered_bytes_rotated": sets * layers * byts}
+        if CPU_BUDGET > 0:
+            # the oracle's fp32 path, 1 thread: one layer's append + attention
+            # over that width's cache (layer 0, set 0)
+            orc = _oracle()
+            hk, hv = rt.download(kcs[0], CTX * bpt), rt.download(vcs[0], CTX * bpt)
+            q = rt.download(b.q_ptr(0, 0), QO_B, np.float32).reshape(1, N_HEAD, HD)
+            nk = rt.download(b.row_ptr(b.d_nk, 0, 0), N_KVH * HD * 4, np.float32)
+            nv = rt.download(b.row_ptr(b.d_nv, 0, 0), N_KVH * HD * 4, np.float32)
+            idx = b.sel_host[0, 0].ravel()
+
+            def one():
+                orc.lib.orc_kv_append(hk.ctypes.data, hv.ctypes.data, nk.ctypes.data,
+                                      nv.ctypes.data, N_KVH * HD, bpt, kind, b.pos[0])
+                orc.attn(q, hk, hv, kind, N_HEAD, N_KVH, HD, 1, idx=idx, width=WIDTH,
+                         tok_stride=N_KVH * WIDTH, kvh_stride=WIDTH, max_kv=CTX,
+                         scale=1.0 / 16, dbl=False, threads=1)
+            t_cpu = _cpu_rate(one, CPU_BUDGET / 2)
+            del hk, hv
+            out[name]["cpu_baseline"] = {
+                "us_per_layer": round(t_cpu * 1e6, 1), "gbs": round(byts / t_cpu / 1e9, 4),
+                "cores": 1, "kind": "port",
+                "sample": "one layer's append + attention (fp32 C restatement, 1 thread)"}
         for p_ in kcs + vcs + [dd]:
             rt.free(p_)
     # session restore: 12 layers x 100000 tokens of q8_0 K and V from pinned memory
@@ -738,6 +837,116 @@ def config_gqa12(b, steps=200, n_head=24):
             "selection_sets": R}
 
 
+def config0(b, steps=300, ctx=4096):
+    """Config 0: one layer, batch 1, a 4096-token q8_0 cache, 16 Q / 2 KV
+    heads: append the new token (q4_hip_kv_append_d, at position 4096), then
+    dense decode attention over all 4097 positions (q4_hip_qsa_decode), with
+    a gate. The call pair is timed per step; the oracle's fp32 path beside
+    it."""
+    rt, lib = b.rt, b.lib
+    max_kv = ctx + 1
+    kc, vc = rt.alloc(max_kv * BPT), rt.alloc(max_kv * BPT)
+    _fill(b, kc, ctx, q4kv.KV_Q8, 6000)
+    _fill(b, vc, ctx, q4kv.KV_Q8, 6001)
+    nk, nv = rt.alloc(N_KVH * HD * 4), rt.alloc(N_KVH * HD * 4)
+    dq, dg, dout = rt.alloc(QO_B), rt.alloc(QO_B), rt.alloc(QO_B)
+    b.gen(nk, N_KVH * HD, 6002)
+    b.gen(nv, N_KVH * HD, 6003)
+    b.gen(dq, N_HEAD * HD, 6004)
+    b.gen(dg, N_HEAD * HD, 6005)
+    lib.q4_hip_pos_push(ctx)
+
+    def enqueue(_r):
+        return (lib.q4_hip_kv_append_d(kc, vc, nk, nv, N_KVH * HD, BPT, q4kv.KV_Q8) and
+                lib.q4_hip_qsa_decode(dq, kc, vc, dg, dout, N_HEAD, N_KVH, HD, max_kv, max_kv,
+                                      1.0 / 16, q4kv.KV_Q8))
+    t, t_graph = _time_both(b, enqueue, 1, steps)
+    byts = 2 * max_kv * BPT + 2 * QO_B + QO_B + APPEND_B  # K, V rows, q, gate, out, append
+    res = {"what": "one layer: q8_0 append at position 4096, then dense decode attention of "
+                   "16 heads over 4097 positions (4096-token cache, gated), per call pair",
+           "us_per_step": _us(t), "graph_us_per_step": _us(t_graph), "bytes_per_step": byts,
+           "gbs": round(byts / t / 1e9, 1)}
+    if CPU_BUDGET > 0:
+        orc = _oracle()
+        rt.sync()
+        hk, hv = rt.download(kc, max_kv * BPT), rt.download(vc, max_kv * BPT)
+        q = rt.download(dq, QO_B, np.float32).reshape(1, N_HEAD, HD)
+        g = rt.download(dg, QO_B, np.float32).reshape(1, N_HEAD, HD)
+        xk = rt.download(nk, N_KVH * HD * 4, np.float32)
+        xv = rt.download(nv, N_KVH * HD * 4, np.float32)
+
+        def one():
+            orc.lib.orc_kv_append(hk.ctypes.data, hv.ctypes.data, xk.ctypes.data,
+                                  xv.ctypes.data, N_KVH * HD, BPT, 2, ctx)
+            orc.attn(q, hk, hv, 2, N_HEAD, N_KVH, HD, 1, gate=g, kv_base=ctx, max_kv=max_kv,
+                     scale=1.0 / 16, dbl=False, threads=1)
+        t_cpu = _cpu_rate(one, CPU_BUDGET)
+        res["cpu_baseline"] = {"us_per_step": round(t_cpu * 1e6, 1),
+                               "gbs": round(byts / t_cpu / 1e9, 4), "cores": 1, "kind": "port",
+                               "sample": "the whole call pair (fp32 C restatement, 1 thread)"}
+    for p_ in (kc, vc, nk, nv, dq, dg, dout):
+        rt.free(p_)
+    return res
+
+
+def config_ref24(b, steps=200, n_head=24):
+    """The reference's one published kernel figure, like for like: its
+    production head layout (24 query / 2 KV heads) through its own per-layer
+    calls, q4_hip_kv_append_d then q4_hip_qsa_decode_idx (one shared 2051-entry
+    list, gated), on config 1's 12 layers of 262144-token q8_0 caches,
+    enqueued directly one layer after the other (and replayed from a
+    captured graph per step). The reference quotes 82 us per decode_idx call
+    on an RX 7900 XTX (its DESIGN.md:130-133)."""
+    rt, lib = b.rt, b.lib
+    L, R = b.L, b.R
+    qb = n_head * HD * 4
+    dq, dg = rt.alloc(R * L * qb), rt.alloc(R * L * qb)
+    b.gen(dq, R * L * n_head * HD, 96)
+    b.gen(dg, R * L * n_head * HD, 97)
+    dout = rt.alloc(L * qb)
+
+    def enqueue(r):
+        ok = True
+        for li in range(L):
+            i = r * L + li
+            ok = ok and lib.q4_hip_kv_append_d(b.kc[li], b.vc[li], b.row_ptr(b.d_nk, r, li),
+                                               b.row_ptr(b.d_nv, r, li), N_KVH * HD, BPT,
+                                               q4kv.KV_Q8)
+            # the shared list: KV head 0's selection of this (set, layer)
+            ok = ok and lib.q4_hip_qsa_decode_idx(dq + i * qb, b.kc[li], b.vc[li], dg + i * qb,
+                                                  dout + li * qb, b.sel_ptr(r, li), WIDTH,
+                                                  n_head, N_KVH, HD, 1, CTX, 1.0 / 16,
+                                                  q4kv.KV_Q8)
+        return ok
+
+    def step(r):
+        lib.q4_hip_pos_push(b.pos[r])
+        return enqueue(r)
+    t = _time_direct(b, step, R, steps)
+    t_graph = None
+    if USE_GRAPHS:
+        graphs = _graphs(lib, enqueue, R)
+        for i in range(max(8, R)):
+            lib.q4_hip_pos_push(b.pos[i % R])
+            assert lib.q4_hip_graph_launch(graphs[i % R])
+        b.rt.sync()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            lib.q4_hip_pos_push(b.pos[i % R])
+            assert lib.q4_hip_graph_launch(graphs[i % R])
+        b.rt.sync()
+        t_graph = (time.perf_counter() - t0) / steps
+        for g in graphs:
+            lib.q4_hip_graph_free(g)
+    for p_ in (dq, dg, dout):
+        rt.free(p_)
+    return {"what": f"per layer q4_hip_kv_append_d + q4_hip_qsa_decode_idx (shared list, "
+                    f"gated), {n_head} Q / {N_KVH} KV heads, {L} layers one after the other",
+            "us_per_layer": _us(t, L), "graph_us_per_layer": _us(t_graph, L),
+            "reference_us_per_call": 82.0,
+            "reference_source": "reference DESIGN.md:130-133, RX 7900 XTX, decode_idx alone"}
+
+
 IDX_RATIO, IDX_KBLK, IDX_HEADS, IDX_DIM = 4, 512, 4, 128
 IDX_ROT, IDX_BASE, IDX_EPS = 64, 1.0e7, 1.0e-6
 
@@ -899,7 +1108,7 @@ def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
             "score_gflop": round(flop / 1e9, 1)}
 
 
-ONLY = {"config2": config2, "config3": config3, "config4": config4, "prep": config_prep,
+ONLY = {"config0": config0, "ref24": config_ref24, "config2": config2, "config3": config3, "config4": config4, "prep": config_prep,
         "gqa12": config_gqa12,
         "out": config_out, "indexer": config_indexer,
         "indexer_prefill": config_indexer_prefill}
@@ -935,8 +1144,10 @@ def main():
                     help="only measure one of the extra configurations and print its JSON "
                          "(for profiling)")
     args = ap.parse_args()
-    global USE_GRAPHS
+    global USE_GRAPHS, CPU_BUDGET
     USE_GRAPHS = bool(args.graphs)
+    if args.cpu_seconds <= 0:
+        CPU_BUDGET = 0.0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the QSA KV path runs on a single MI355X "
               "(no collectives); run with --gpus 1", file=sys.stderr)
@@ -972,9 +1183,11 @@ def main():
     g_us, g_gbs = b.gather_ceiling()
     configs = None
     if args.configs:
-        configs = {"config2_batched_decode": config2(b), "config3_chunked_prefill": config3(b),
+        configs = {"config0_dense_decode": config0(b),
+                   "config2_batched_decode": config2(b), "config3_chunked_prefill": config3(b),
                    "config4_widths_restore": config4(b),
                    "production_heads_24_2": config_gqa12(b),
+                   "reference_call_24q_2kv": config_ref24(b),
                    "qk_prep_fused_step": config_prep(b),
                    "out_projection_fused": config_out(b),
                    "indexer_decode": config_indexer(b),

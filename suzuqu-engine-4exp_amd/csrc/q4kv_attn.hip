@@ -3102,7 +3102,9 @@ static void choose_split(uint32_t n_items, uint32_t n_chunks, uint32_t gqa, bool
     S = (split_target() + n_items - 1u) / n_items;
     if (S > n_chunks) S = n_chunks;
     if (S < 1u) S = 1u;
-    if (S > COMB_MAXS) S = COMB_MAXS;
+    /* at most COMB_REG splits: the merge then holds every partial in
+     * registers (one memory round trip; past that it walks them) */
+    if (S > COMB_REG) S = COMB_REG;
     const size_t per = (size_t)gqa * PSTRIDE;
     while (S > 1u && (size_t)n_items * S * per > cap) S--;
     if (!have_part) S = 1u;
