@@ -1478,8 +1478,11 @@ __device__ static inline uint32_t lds_u16x2(const uint8_t *a, const uint8_t *b) 
     return (uint32_t)*(const uint16_t *)a | ((uint32_t)*(const uint16_t *)b << 16);
 }
 
-template <int MODE, int HG>
+/* APP: the launch also performs a held append of one token's K/V rows at
+ * the device position (as the step modes do with a descriptor's rows). */
+template <int MODE, int HG, bool APP = false>
 __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
+    constexpr bool STEPL = IS_STEP(MODE) || APP; /* a token's rows are appended */
     constexpr uint32_t ROWB = 272, NCH = 17;
     constexpr uint32_t NSLAB = 4u / HG, NE = NSLAB * SLAB; /* slabs, entries per pass */
     constexpr uint32_t RBYTES = 2u * NE * ROWB;           /* K rows | V rows */
@@ -1507,7 +1510,12 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     uint32_t s, item;
     if (!xcd_slot(a, s, item)) return; /* padding of the last group row */
     const uint32_t gqa = a.n_head / a.n_kvh, kh = item % a.n_kvh;
-    const Item it = resolve_item<MODE>(a, item);
+    Item it = resolve_item<MODE>(a, item);
+    if (APP) {
+        it.knew = a.app_k + (size_t)kh * 256u;
+        it.vnew = a.app_v + (size_t)kh * 256u;
+        it.pos_new = (uint32_t)ldg(a.app_pos);
+    }
     const uint32_t c = lane & 15u, jg = lane >> 4; /* MFMA column / row, k-group */
     const float nsel = c >= 8u ? -1.f : 0.f;
     const size_t rstride = (size_t)a.n_kvh * ROWB;
@@ -1537,7 +1545,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
      * the quantised rows to the caches, and a wave whose slab lists the
      * position uses the same bytes in LDS instead of the fetched row. */
     float nk[4] = {0.f, 0.f, 0.f, 0.f}, nv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (IS_STEP(MODE)) {
+    if (STEPL) {
         const uint32_t off = 32u * (lane >> 3) + 4u * (lane & 7u);
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) {
@@ -1675,7 +1683,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         TRACEW(3);
         if (HG > 1) __syncthreads(); /* the head-group waves share the slab's rows */
         if (hg == 0u && any) {
-            if (IS_STEP(MODE)) {
+            if (STEPL) {
                 /* rows at the appended position take the new token's bytes */
                 uint64_t hit = __ballot(lane < 32u && pos >= 0 && (uint32_t)pos == it.pos_new);
                 if (hit) {
@@ -1904,7 +1912,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     }
     /* MODE_STEP: split 0 writes the quantised rows (K after its prep) last,
      * so no wait inside the kernel covers these stores */
-    if (IS_STEP(MODE) && s == 0u && wave == 0u && it.pos_new < it.max_kv) {
+    if (STEPL && s == 0u && wave == 0u && (APP ? item < a.n_kvh : it.pos_new < it.max_kv)) {
         int q[4];
         float d = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
         q8_lane_store((uint8_t *)kbase + (size_t)it.pos_new * rstride + 34u * (lane >> 3),
@@ -3482,8 +3490,12 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
      * it first */
     bool app = false;
     if constexpr (KIND == Q4KV_Q8 && (MODE == MODE_INDEXED || MODE == MODE_DENSE)) {
-        app = fast && !pl.slab && cps < db_min_chunks() && n_items <= Q4KV_MAX_GRID_Y &&
-              held_matches(a);
+        /* the chunk kernel's single-buffer instance, or the slab kernel on
+         * decode-sized launches (prefill-sized ones run the band kernel
+         * first, which reads the rows without the substitution) */
+        app = a.hd == 256u && n_items <= 64u && held_matches(a) &&
+              ((fast && !pl.slab && cps < db_min_chunks()) ||
+               (pl.slab && gqa <= 16u && !(S == 1u && gqa <= 8u)));
         if (app) {
             a.app_k = q4kv_held.k;
             a.app_v = q4kv_held.v;
@@ -3538,7 +3550,14 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
             qsa_h16_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (pl.h16)
             qsa_h16_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
-        else if (pl.slab && pl.hg == 1u)
+        else if (pl.slab && app) {
+            if constexpr (MODE == MODE_INDEXED || MODE == MODE_DENSE) {
+                if (pl.hg == 1u)
+                    qsa_slab_k<MODE, 1, true><<<grid, 256, 0, q4kv_stream>>>(a);
+                else
+                    qsa_slab_k<MODE, 2, true><<<grid, 256, 0, q4kv_stream>>>(a);
+            }
+        } else if (pl.slab && pl.hg == 1u)
             qsa_slab_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (pl.slab)
             qsa_slab_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);

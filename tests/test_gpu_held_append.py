@@ -55,7 +55,8 @@ def _append_oracle(oracle, hk, hv, k, v, n, bpt, pos):
                              bpt, 2, pos)
 
 
-@pytest.mark.parametrize("n_head,gated", [(16, False), (16, True), (8, False)])
+# 8 query heads per KV head (the chunk kernel), 4 (chunk), 12 (the slab kernel)
+@pytest.mark.parametrize("n_head,gated", [(16, False), (16, True), (8, False), (24, True)])
 def test_held_append_performed_by_the_decode(rt, oracle, n_head, gated):
     """append_d then decode_idx_kv at consecutive positions: the new rows
     bit-exact in both caches and seen by the decode of the same call pair."""
