@@ -167,7 +167,10 @@ bool q4_hip_qsa_decode_idx_kv(const float *d_q, const void *d_kcache, const void
 /* One decode item of a batched launch: an independent sequence (or layer)
  * with its own caches, query, output and per-KV-head position lists.
  * All pointers are device pointers; the descriptor array itself lives in
- * device memory (caller-owned, 64 bytes per entry). */
+ * device memory (caller-owned, 64 bytes per entry). kcache and vcache must
+ * be 16-byte aligned (the batched kernels fetch rows in 16-byte pieces;
+ * q4_hip_malloc memory always is): the library cannot read the descriptors
+ * on the host to check. */
 typedef struct {
     const void *kcache;     /* [max_kv][n_kvh][row] */
     const void *vcache;

@@ -3291,7 +3291,7 @@ static uint32_t any_splits(uint32_t n_items, uint32_t max_n, uint32_t gqa, bool 
     const uint64_t wgs = (uint64_t)n_items * hc;
     uint32_t S = wgs >= split_target() ? 1u : (uint32_t)((split_target() + wgs - 1u) / wgs);
     if (S > n_iter) S = n_iter;
-    if (S > COMB_MAXS) S = COMB_MAXS;
+    if (S > COMB_REG) S = COMB_REG; /* the merge's register path */
     const size_t per = (size_t)gqa * PSTRIDE;
     while (S > 1u && (size_t)n_items * S * per > cap) S--;
     return have_part && S >= 1u ? S : 1u;
@@ -3301,6 +3301,10 @@ template <int KIND, int MODE>
 static bool launch_any(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gqa, PartBuf pb) {
     const uint32_t hc = (gqa + ANY_HEADS - 1u) / ANY_HEADS;
     const uint32_t S = any_splits(n_items, max_n, gqa, pb.ptr != nullptr, pb.cap);
+    if (S > 1u && (size_t)n_items * S * gqa * PSTRIDE > pb.cap) {
+        Q4KV_ERR("qsa attention: %u splits of %u items exceed the partial buffer", S, n_items);
+        return false;
+    }
     a.S = S;
     a.cps = 0u;
     a.part = pb.ptr;
@@ -3370,7 +3374,7 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
         } else {
             S = n_items >= SLAB_MAX_WG ? 1u : SLAB_MAX_WG / n_items;
             if (S < 1u) S = 1u;
-            if (S > COMB_MAXS) S = COMB_MAXS;
+            if (S > COMB_REG) S = COMB_REG; /* the merge's register path */
             const size_t per = (size_t)gqa * PSTRIDE;
             while (S > 1u && (size_t)n_items * S * per > cap) S--;
             if (!have_part) S = 1u;
@@ -3404,7 +3408,7 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
         } else {
             S = n_items >= SLAB_MAX_WG ? 1u : SLAB_MAX_WG / n_items;
             if (S < 1u) S = 1u;
-            if (S > COMB_MAXS) S = COMB_MAXS;
+            if (S > COMB_REG) S = COMB_REG; /* the merge's register path */
             const size_t per = (size_t)gqa * PSTRIDE;
             while (S > 1u && (size_t)n_items * S * per > cap) S--; /* waves then loop */
             if (!have_part) S = 1u;
@@ -3485,6 +3489,10 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap, rows16);
     if (IS_STEP(MODE) && !fast && !pl.slab && !pl.h16 && !pl.f32w) return false; /* the fused append needs these */
     const uint32_t S = pl.S, cps = pl.cps;
+    if (S > 1u && (!pb.ptr || (size_t)n_items * S * gqa * PSTRIDE > pb.cap)) {
+        Q4KV_ERR("qsa attention: %u splits of %u items exceed the partial buffer", S, n_items);
+        return false;
+    }
     /* a held append on these caches rides in the chunk kernel's launch (one
      * launch pass: the split kernel then the merge); any other launch runs
      * it first */
@@ -3697,6 +3705,22 @@ extern "C" bool q4_hip_qsa_decode_batch(const q4kv_seq_desc *d_descs, uint32_t n
     return launch_attn<MODE_BATCH>(kv_f16, a, n_seq * n_kvh, max_n);
 }
 
+/* The split plan q4_hip_qsa_step_batch's launch takes for these arguments
+ * (the dispatch of step_batch below, then launch_kind's plan_launch). */
+static Plan step_batch_plan(int kind, uint32_t hd, uint32_t n_items, uint32_t max_n,
+                            uint32_t gqa, bool have, size_t cap) {
+    if (any_shape(hd, gqa)) return Plan{false, 1u, any_splits(n_items, max_n, gqa, have, cap), 0u};
+    if (step_fusable(kind, hd, gqa) && kind == Q4KV_F16)
+        return plan_launch<Q4KV_F16, MODE_STEP>(hd, n_items, max_n, gqa, have, cap);
+    if (step_fusable(kind, hd, gqa) && kind == Q4KV_F32)
+        return plan_launch<Q4KV_F32, MODE_STEP>(hd, n_items, max_n, gqa, have, cap);
+    if (step_fusable(kind, hd, gqa))
+        return plan_launch<Q4KV_Q8, MODE_STEP>(hd, n_items, max_n, gqa, have, cap);
+    if (kind == Q4KV_F32) return plan_launch<Q4KV_F32, MODE_BATCH>(hd, n_items, max_n, gqa, have, cap);
+    if (kind == Q4KV_F16) return plan_launch<Q4KV_F16, MODE_BATCH>(hd, n_items, max_n, gqa, have, cap);
+    return plan_launch<Q4KV_Q8, MODE_BATCH>(hd, n_items, max_n, gqa, have, cap);
+}
+
 static bool step_batch(const q4kv_step_desc *d_descs, uint32_t n_seq, uint32_t n_head,
                        uint32_t n_kvh, uint32_t hd, float scale, int kv_f16, uint32_t max_n,
                        PartBuf pb) {
@@ -3774,24 +3798,13 @@ extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uin
         Q4KV_ERR("qsa_step_batch_noalloc: scratch not resolved on this device (q4_hip_init)");
         return false;
     }
-    /* the same split division as q4_hip_qsa_step_batch (so the same results),
-     * which must fit the static scratch */
+    /* the split division q4_hip_qsa_step_batch takes with the library's
+     * buffer (so the same results) must fit the static scratch; planned on
+     * the scratch's own capacity it is then the same division (every larger
+     * split count misses the larger buffer too) */
     const uint32_t gqa = n_head / n_kvh, n_items = n_seq * n_kvh;
-    const bool have = q4kv_part != nullptr;
-    const Plan pl =
-        any_shape(hd, gqa)
-            ? Plan{false, 1u, any_splits(n_items, max_n, gqa, have, q4kv_part_cap), 0u}
-        : step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F16
-            ? plan_launch<Q4KV_F16, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
-        : step_fusable(kv_f16, hd, gqa) && kv_f16 == Q4KV_F32
-            ? plan_launch<Q4KV_F32, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
-        : step_fusable(kv_f16, hd, gqa)
-            ? plan_launch<Q4KV_Q8, MODE_STEP>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
-        : kv_f16 == Q4KV_F32
-            ? plan_launch<Q4KV_F32, MODE_BATCH>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
-        : kv_f16 == Q4KV_F16
-            ? plan_launch<Q4KV_F16, MODE_BATCH>(hd, n_items, max_n, gqa, have, q4kv_part_cap)
-            : plan_launch<Q4KV_Q8, MODE_BATCH>(hd, n_items, max_n, gqa, have, q4kv_part_cap);
+    const Plan pl = step_batch_plan(kv_f16, hd, n_items, max_n, gqa, q4kv_part != nullptr,
+                                    q4kv_part_cap);
     const uint32_t S = pl.S;
     const size_t need = S > 1u ? (size_t)n_items * S * gqa * PSTRIDE : 0u;
     if (need > Q4KV_SCRATCH_FLOATS) {
@@ -3801,7 +3814,7 @@ extern "C" bool q4_hip_qsa_step_batch_noalloc(const q4kv_step_desc *d_descs, uin
         return false;
     }
     return step_batch(d_descs, n_seq, n_head, n_kvh, hd, scale, kv_f16, max_n,
-                      PartBuf{g_scratch_ptr[dev], q4kv_part_cap});
+                      PartBuf{g_scratch_ptr[dev], Q4KV_SCRATCH_FLOATS});
 }
 
 #ifdef Q4KV_TRACE

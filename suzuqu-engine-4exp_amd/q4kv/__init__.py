@@ -24,13 +24,23 @@ _u32, _u64, _i32, _f32, _b = C.c_uint32, C.c_uint64, C.c_int32, C.c_float, C.c_b
 
 
 class SeqDesc(C.Structure):
-    """One entry of the q4kv_seq_desc array (64 bytes), see include/q4kv.h."""
+    """One entry of the q4kv_seq_desc array (64 bytes), see include/q4kv.h.
+    The batched kernels fetch cache rows in 16-byte pieces, so the caches a
+    descriptor names must be 16-byte aligned (include/q4kv.h); construction
+    refuses others (device memory from q4_hip_malloc always is)."""
 
     _fields_ = [
         ("kcache", _vp), ("vcache", _vp), ("q", _vp), ("gate", _vp), ("out", _vp),
         ("idx", _vp), ("n_sel", _u32), ("idx_kvh_stride", _u32), ("max_kv", _u32),
         ("reserved", _u32),
     ]
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        for name in ("kcache", "vcache"):
+            ptr = getattr(self, name) or 0
+            if ptr % 16:
+                raise ValueError(f"q4kv_seq_desc.{name} must be 16-byte aligned (got {ptr:#x})")
 
 
 assert C.sizeof(SeqDesc) == 64
