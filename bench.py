@@ -1215,6 +1215,8 @@ def main():
         },
         "us_per_layer": round(wall / (K * L) * 1e6, 4),
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+        "timing_mode": ("direct enqueue of each step's calls on the library stream; the "
+                        "captured-graph replay of the same steps is the *_graph_* keys"),
     }
     for mode, (w, g, _) in res.items():
         out[f"{mode}_us_per_layer"] = round(w / (K * L) * 1e6, 4)

@@ -988,10 +988,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
 #pragma unroll
         for (uint32_t i = 0; i < 4u; i++) nx[i] = ldg(src + i);
     }
-    /* the quantised bytes of the new rows (computed once, with the row DMA
-     * in flight; MODE_PSTEP after the key preparation below) */
-    int nq[4] = {0, 0, 0, 0};
-    float nd = 0.f;
+
     if (MODE == MODE_PSTEP && wave == 0) {
         /* wave 0 holds the K row (lane l: dims 4l .. 4l+3): RMSNorm + RoPE
          * at the token's position, through LDS in the shared prep layout */
@@ -1036,8 +1033,6 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
      * those too */
     asm volatile("" ::: "memory");
     if (c0 < c1) pos_issue<NLD + 1, MODE>(it, jcur, raw);
-    /* with the Q and index loads in flight */
-    if (step_lane) nd = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], nq);
     if (MODE == MODE_PSTEP && s == 0u && it.gate) {
         /* the gate halves of the [q | gate] rows go to the gate buffer the
          * merge reads */
@@ -1138,6 +1133,8 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             uint64_t mm = (uint64_t)s_subst[0] | ((uint64_t)s_subst[1] << 32);
             if (mm) {
                 if (step_lane) {
+                    int nq[4];
+                    const float nd = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], nq);
                     uint8_t *base = (tid < 64u ? kraw : vraw) + 34u * ((tid >> 3) & 7u);
                     for (; mm; mm &= mm - 1u)
                         q8_lane_store(base + (uint32_t)__builtin_ctzll(mm) * ROWB, tid & 7u, nd,
@@ -1385,6 +1382,8 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
      * took the same bytes in LDS) */
     const bool writer = s == 0u && (!APP || item < a.n_kvh);
     if (STEPL && writer && (APP || it.pos_new < it.max_kv) && step_lane) {
+        int nq[4];
+        const float nd = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], nq);
         uint8_t *row = (uint8_t *)(tid < 64u ? kbase : vbase) + (size_t)it.pos_new * rstride;
         q8_lane_store(row + 34u * ((tid >> 3) & 7u), tid & 7u, nd, nq);
     }
