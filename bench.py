@@ -455,6 +455,20 @@ def config2(b, steps=200, sets=10):
     t, t_graph = _time_both(b, lambda r: lib.q4_hip_qsa_step_batch(
         dd + r * n_seq * sz, n_seq, N_HEAD, N_KVH, HD, 1.0 / 16, q4kv.KV_Q8, WIDTH), sets, steps)
     byts = n_seq * LAYER_B
+    # the gather ceiling of this step's rows: the same K/V rows of every
+    # sequence DMA'd to LDS with no compute, one launch per step, the sets
+    # rotating as in the timed steps
+    n = sets * n_seq
+    tabs = [(C.c_void_p * n)(*[caches[i % n_seq][j] for i in range(n)]) for j in (0, 1)]
+    tabs.append((C.c_void_p * n)(*[dsel + i * IDX_B for i in range(n)]))
+    dtabs = [rt.alloc(8 * n) for _ in range(3)]
+    for dp, arr in zip(dtabs, tabs):
+        assert lib.q4_hip_h2d(dp, C.addressof(arr), 8 * n)
+    rt.sync()
+    g_us = b.synth.q4kv_gather_probe_us(dtabs[0], dtabs[1], dtabs[2], n_seq, sets, N_KVH, WIDTH,
+                                        400)
+    for dp in dtabs:
+        rt.free(dp)
     cpu = None
     if CPU_BUDGET > 0:
         # the oracle's fp32 path (1 thread) on 4 of the 32 sequences (their
@@ -498,6 +512,11 @@ def config2(b, steps=200, sets=10):
             "gbs": round(byts / t / 1e9, 1), "pct_of_peak": round(100 * byts / t / 1e9 / PEAK_GBS, 2),
             "steps": steps, "selection_sets": sets,
             "gathered_bytes_rotated": sets * byts,
+            "gather_ceiling": {"us_per_step": round(g_us, 2),
+                               "gbs": round(n_seq * GATHER_B / (g_us * 1e-6) / 1e9, 1),
+                               "frac_reached": round(g_us * 1e-6 / t, 3),
+                               "what": "the step's K/V rows DMA'd to LDS with no compute, one "
+                                       "launch per step (the headline's probe)"},
             "note": "sets rotate so the rows gathered across sets exceed the 256 MB Infinity Cache"}
 
 
