@@ -1092,13 +1092,15 @@ def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
     rt.sync()
 
     def run():
-        ok = lib.q4_hip_qsa_pool(raw, pool, wn, IDX_DIM, IDX_RATIO, 0, nb, IDX_ROT, IDX_BASE,
-                                 IDX_EPS)
+        # the chunk's raw indexer queries, as their projection would leave them
+        # (one copy: q4_hip_copy blocks until it lands, so per-slice copies
+        # would time host round trips, not the indexer)
+        ok = lib.q4_hip_copy(q, tmp, chunk * IDX_HEADS * IDX_DIM)
+        ok &= lib.q4_hip_qsa_pool(raw, pool, wn, IDX_DIM, IDX_RATIO, 0, nb, IDX_ROT, IDX_BASE,
+                                  IDX_EPS)
         for s0 in range(0, chunk, slice_):
             pos0 = cache + s0
             qs = q + s0 * IDX_HEADS * IDX_DIM * 4
-            ok &= lib.q4_hip_copy(qs, tmp + s0 * IDX_HEADS * IDX_DIM * 4,
-                                  slice_ * IDX_HEADS * IDX_DIM)
             ok &= lib.q4_hip_qsa_k_prep_n(qs, wn, IDX_HEADS, IDX_DIM, IDX_ROT, pos0, IDX_BASE,
                                           IDX_EPS, slice_)
             n_blocks = (pos0 + slice_) // IDX_RATIO
