@@ -1069,6 +1069,102 @@ def config_indexer(b, steps=100, layers=12):
     return out
 
 
+def config_layer(b, steps=100):
+    """One decode token's whole QSA KV path per layer, in the reference's call
+    order (src/q4_fwd.c:891-922): q4_hip_kv_append_d of the new K/V rows, the
+    indexer (the raw key store, the pooling of the block it completes, the
+    indexer query's RMSNorm + RoPE, scores of the 65536 visible blocks, the
+    top-512 selection expanded to 2051 positions), then
+    q4_hip_qsa_decode_idx over that shared list (16 query / 2 KV heads,
+    gated) on config 1's 262144-token q8_0 caches; the layers one after the
+    other. "separate": the reference's five indexer calls; "fused": the
+    indexer's store, pool, prep and scores in one q4_hip_qsa_index_score_d.
+    The held append rides in the indexer's first launch either way."""
+    rt, lib = b.rt, b.lib
+    L, R = b.L, b.R
+    max_blocks = CTX // IDX_RATIO
+    raws, pools, scs, sels, qs, ks = [], [], [], [], [], []
+    tmp = rt.alloc(CTX * IDX_DIM * 4)
+    wn = rt.alloc(IDX_DIM * 4)
+    b.gen(wn, IDX_DIM, 78)
+    for li in range(L):
+        raw = rt.alloc(CTX * IDX_DIM * 2)
+        b.gen(tmp, CTX * IDX_DIM, 9400 + li)
+        assert lib.q4_hip_f32_to_f16(raw, tmp, CTX * IDX_DIM)
+        raws.append(raw)
+        pools.append(rt.alloc(max_blocks * IDX_DIM * 4))
+        assert lib.q4_hip_qsa_pool(raw, pools[-1], wn, IDX_DIM, IDX_RATIO, 0, max_blocks,
+                                   IDX_ROT, IDX_BASE, IDX_EPS)
+        scs.append(rt.alloc(max_blocks * 4))
+        sels.append(rt.alloc(WIDTH * 4))
+        q = rt.alloc(R * IDX_HEADS * IDX_DIM * 4)
+        b.gen(q, R * IDX_HEADS * IDX_DIM, 9500 + li)
+        qs.append(q)
+        k = rt.alloc(R * IDX_DIM * 4)
+        b.gen(k, R * IDX_DIM, 9600 + li)
+        ks.append(k)
+    rt.sync()
+    rt.free(tmp)
+    dg = rt.alloc(R * L * QO_B)
+    b.gen(dg, R * L * N_HEAD * HD, 98)
+    qsz, ksz = IDX_HEADS * IDX_DIM * 4, IDX_DIM * 4
+
+    def enqueue(r, fused):
+        ok = True
+        for li in range(L):
+            ok = ok and lib.q4_hip_kv_append_d(b.kc[li], b.vc[li], b.row_ptr(b.d_nk, r, li),
+                                               b.row_ptr(b.d_nv, r, li), N_KVH * HD, BPT,
+                                               q4kv.KV_Q8)
+            iq, ik = qs[li] + r * qsz, ks[li] + r * ksz
+            if fused:
+                ok = ok and lib.q4_hip_qsa_index_score_d(raws[li], pools[li], wn, ik, iq, wn,
+                                                         scs[li], max_blocks, IDX_HEADS,
+                                                         IDX_DIM, IDX_RATIO, IDX_ROT, IDX_BASE,
+                                                         IDX_EPS)
+            else:
+                ok = ok and lib.q4_hip_f32_to_f16_d(raws[li], IDX_DIM, ik, IDX_DIM)
+                ok = ok and lib.q4_hip_qsa_pool_d(raws[li], pools[li], wn, IDX_DIM, IDX_RATIO,
+                                                  IDX_ROT, IDX_BASE, IDX_EPS)
+                ok = ok and lib.q4_hip_qsa_k_prep_d(iq, wn, IDX_HEADS, IDX_DIM, IDX_ROT,
+                                                    IDX_BASE, IDX_EPS)
+                ok = ok and lib.q4_hip_qsa_score_d(iq, pools[li], scs[li], max_blocks,
+                                                   IDX_HEADS, IDX_DIM, IDX_RATIO)
+            ok = ok and lib.q4_hip_qsa_topk_d(scs[li], sels[li], max_blocks, IDX_KBLK,
+                                              IDX_RATIO, WIDTH)
+            ok = ok and lib.q4_hip_qsa_decode_idx(b.q_ptr(r, li), b.kc[li], b.vc[li],
+                                                  dg + (r * L + li) * QO_B,
+                                                  b.d_out + li * QO_B, sels[li], WIDTH, N_HEAD,
+                                                  N_KVH, HD, 1, CTX, 1.0 / 16, q4kv.KV_Q8)
+        return ok
+
+    out = {"what": f"per layer: q4_hip_kv_append_d, the indexer (65536 visible blocks, "
+                   f"top-512 -> 2051 positions), q4_hip_qsa_decode_idx over its list (gated, "
+                   f"{N_HEAD} Q / {N_KVH} KV heads, ctx {CTX}); {L} layers one after the other",
+           "launches_per_layer": {"separate": 7, "fused": 4}}
+    for name, fused in (("separate", False), ("fused", True)):
+        def step(r, fused=fused):
+            lib.q4_hip_pos_push(b.pos[r])
+            return enqueue(r, fused)
+        out[f"{name}_us_per_layer"] = _us(_time_direct(b, step, R, steps), L)
+        if USE_GRAPHS:
+            graphs = _graphs(lib, lambda r, fused=fused: enqueue(r, fused), R)
+            for i in range(max(8, R)):
+                lib.q4_hip_pos_push(b.pos[i % R])
+                assert lib.q4_hip_graph_launch(graphs[i % R])
+            rt.sync()
+            t0 = time.perf_counter()
+            for i in range(steps):
+                lib.q4_hip_pos_push(b.pos[i % R])
+                assert lib.q4_hip_graph_launch(graphs[i % R])
+            rt.sync()
+            out[f"{name}_graph_us_per_layer"] = _us((time.perf_counter() - t0) / steps, L)
+            for g in graphs:
+                lib.q4_hip_graph_free(g)
+    for p_ in raws + pools + scs + sels + qs + ks + [wn, dg]:
+        rt.free(p_)
+    return out
+
+
 def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
     """The indexer of config 3's chunked prefill (src/q4_fwd.c:740-770, sliced by 512
     tokens as src/q4_fwd.c:1744-1754): for each 512-token slice of an 8192-token
@@ -1132,7 +1228,7 @@ def config_indexer_prefill(b, cache=16384, chunk=8192, slice_=512, reps=3):
 ONLY = {"config0": config0, "ref24": config_ref24, "config2": config2, "config3": config3, "config4": config4, "prep": config_prep,
         "gqa12": config_gqa12,
         "out": config_out, "indexer": config_indexer,
-        "indexer_prefill": config_indexer_prefill}
+        "indexer_prefill": config_indexer_prefill, "layer": config_layer}
 
 
 def _cpu_model():
@@ -1212,7 +1308,8 @@ def main():
                    "qk_prep_fused_step": config_prep(b),
                    "out_projection_fused": config_out(b),
                    "indexer_decode": config_indexer(b),
-                   "indexer_prefill": config_indexer_prefill(b)}
+                   "indexer_prefill": config_indexer_prefill(b),
+                   "reference_layer_sequence": config_layer(b)}
     threads = min(16, len(os.sched_getaffinity(0)))
     parity, cpu = b.check_and_cpu(args.cpu_seconds, threads)
     head = "batched" if "batched" in res else "sequential"

@@ -137,9 +137,15 @@ __global__ __launch_bounds__(64) void qsa_pool_dk(const uint32_t *raw2, float *p
 }
 
 /* fp16 store of the raw key at the device position's row
- * (src/q4_rocm.cu:7932-7947). */
+ * (src/q4_rocm.cu:7932-7947) by the first n_wg workgroups; any after them
+ * write a held cache append (app). */
 __global__ __launch_bounds__(256) void f16_at_k(const float *src, __half *dst0, uint32_t stride,
-                                                uint64_t n, const int32_t *pp) {
+                                                uint64_t n, const int32_t *pp, uint32_t n_wg,
+                                                q4kv_app_args app) {
+    if (blockIdx.x >= n_wg) {
+        q4kv_app_wg(app, blockIdx.x - n_wg);
+        return;
+    }
     __half *dst = dst0 + (size_t)(uint32_t)*pp * stride;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = __float2half_rn(ldg(src + i));
@@ -213,8 +219,8 @@ __device__ __attribute__((always_inline)) inline void score_store(const float4 (
 __device__ __attribute__((always_inline)) inline void score_rows(const float4 (&qr)[4][4], const float *pool, float *srow,
                                   uint32_t rb, uint32_t n_blocks, uint32_t n_vis,
                                   uint32_t lane, uint32_t wave, float4 nr0, float4 nr1,
-                                  float4 nr2, float4 nr3, uint32_t b_new) {
-    for (; rb < n_blocks; rb += gridDim.x * SC_ROWS_WG) {
+                                  float4 nr2, float4 nr3, uint32_t b_new, uint32_t n_wg) {
+    for (; rb < n_blocks; rb += n_wg * SC_ROWS_WG) {
         float4 p[2][4];
         score_load(p, pool, rb, n_vis, lane, wave);
         score_store(qr, p, srow, rb, n_blocks, n_vis, lane, wave, nr0, nr1, nr2, nr3, b_new);
@@ -252,7 +258,7 @@ __global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float
                            : make_float4(0.f, 0.f, 0.f, 0.f);
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     score_rows(qr, pool, score + (size_t)t * stride, rb, n_blocks, n_vis, lane, wave, z, z, z, z,
-               0xffffffffu);
+               0xffffffffu, gridDim.x);
 }
 
 /* The decode indexer step in one launch (no reference counterpart; it is
@@ -263,7 +269,8 @@ __global__ __launch_bounds__(256) void qsa_score_v_k(const float *q, const float
  * into LDS); the workgroup whose rows hold the block this position
  * completes pools it (with the new key's fp16 row in place of the stored
  * one) and writes it to the pool; then every workgroup scores its 64 rows.
- * q is read, not modified. */
+ * q is read, not modified. The first n_wg workgroups do this; any after them
+ * write a held cache append (app). */
 template <bool BATCH>
 __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float *pool,
                                                           const float *wn_k, const float *k_new,
@@ -272,7 +279,12 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
                                                           uint32_t ratio, uint32_t n_rot,
                                                           float base, float eps,
                                                           const int32_t *pp,
-                                                          const q4kv_index_desc *descs) {
+                                                          const q4kv_index_desc *descs,
+                                                          uint32_t n_wg, q4kv_app_args app) {
+    if (!BATCH && blockIdx.x >= n_wg) {
+        q4kv_app_wg(app, blockIdx.x - n_wg);
+        return;
+    }
     __shared__ float qs[4][IDX_HD];
     __shared__ float new_row[IDX_HD];
     uint32_t pos;
@@ -327,7 +339,7 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
     const bool completes = (pos + 1) % ratio == 0;
     const uint32_t b_new = completes ? n_vis - 1 : 0xffffffffu;
     /* the workgroup whose grid-stride row groups hold b_new pools it */
-    if (completes && (b_new / SC_ROWS_WG) % gridDim.x == blockIdx.x && wave == 0) {
+    if (completes && (b_new / SC_ROWS_WG) % n_wg == blockIdx.x && wave == 0) {
         const float2 v = pool_block(raw2, pool, wn_k, ratio, b_new, n_rot, freq, eps, lane,
                                     true, kh);
         new_row[2 * lane] = v.x;
@@ -343,8 +355,8 @@ __global__ __launch_bounds__(256) void qsa_index_score_dk(uint32_t *raw2, float 
 #pragma unroll
     for (int i = 0; i < 4; i++) nr[i] = *(const float4 *)&new_row[32 * i + 4 * g];
     score_store(qr, p, score, rb, n_vis, n_vis, lane, wave, nr[0], nr[1], nr[2], nr[3], b_new);
-    score_rows(qr, pool, score, rb + gridDim.x * SC_ROWS_WG, n_vis, n_vis, lane, wave, nr[0],
-               nr[1], nr[2], nr[3], b_new);
+    score_rows(qr, pool, score, rb + n_wg * SC_ROWS_WG, n_vis, n_vis, lane, wave, nr[0],
+               nr[1], nr[2], nr[3], b_new, n_wg);
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -1007,15 +1019,20 @@ extern "C" bool q4_hip_qsa_k_prep_d(float *d_k, const float *d_wn, uint32_t n_kv
                        "qsa_k_prep_d");
 }
 
+/* The first call after a held q4_hip_kv_append_d in the reference's decode
+ * order (src/q4_fwd.c:891-905): this launch carries the held append. */
 extern "C" bool q4_hip_f32_to_f16_d(void *dst_base, uint32_t stride_elems, const float *src,
                                     uint64_t n) {
-    Q4KV_FLUSH_OR_FAIL();
-    if (!q4kv_ok || !q4kv_pos_d || !dst_base || !src || !n) return false;
     const uint64_t grid = (n + 255u) / 256u;
-    if (grid > 0x7fffffffull) return false;
+    if (!q4kv_ok || !q4kv_pos_d || !dst_base || !src || !n || grid > 0x7fffffffull) {
+        Q4KV_FLUSH_OR_FAIL();
+        return false;
+    }
+    q4kv_app_args app{};
+    const uint32_t extra = q4kv_take_held(&app);
     (void)hipGetLastError();
-    f16_at_k<<<(uint32_t)grid, 256, 0, q4kv_stream>>>(src, (__half *)dst_base, stride_elems, n,
-                                                      q4kv_pos_d);
+    f16_at_k<<<(uint32_t)grid + extra, 256, 0, q4kv_stream>>>(
+        src, (__half *)dst_base, stride_elems, n, q4kv_pos_d, (uint32_t)grid, app);
     return q4kv_launch_ok("f32_to_f16_d");
 }
 
@@ -1148,22 +1165,27 @@ extern "C" bool q4_hip_qsa_index_score_d(void *raw_f16, float *pool, const float
                                          float *score, uint32_t stride, uint32_t n_head,
                                          uint32_t hd, uint32_t ratio, uint32_t n_rot,
                                          float rope_base, float eps) {
-    Q4KV_FLUSH_OR_FAIL();
     if (!q4kv_ok || !q4kv_pos_d || !raw_f16 || !pool || !k_new || !q || !score ||
-        hd != IDX_HD || n_head == 0 || n_head > 4 || ratio == 0 || n_rot > hd)
+        hd != IDX_HD || n_head == 0 || n_head > 4 || ratio == 0 || n_rot > hd) {
+        Q4KV_FLUSH_OR_FAIL();
         return false;
+    }
     if (((uintptr_t)raw_f16 & 3u) || ((uintptr_t)pool & 15u) || ((uintptr_t)q & 15u) ||
         ((uintptr_t)k_new & 7u) || ((uintptr_t)wn_k & 7u) || ((uintptr_t)wn_q & 7u)) {
+        Q4KV_FLUSH_OR_FAIL();
         Q4KV_ERR("qsa_index_score_d: misaligned buffer");
         return false;
     }
-    if (stride == 0) return true;
+    if (stride == 0) return q4kv_flush();
+    /* the first call after a held q4_hip_kv_append_d in the fused decode
+     * order: this launch carries the held append */
+    q4kv_app_args app{};
+    const uint32_t extra = q4kv_take_held(&app);
     (void)hipGetLastError();
     const uint32_t gx = (stride + SC_ROWS_WG - 1) / SC_ROWS_WG;
-    qsa_index_score_dk<false><<<gx, 256, 0, q4kv_stream>>>((uint32_t *)raw_f16, pool, wn_k,
-                                                           k_new, q, wn_q, score, n_head, ratio,
-                                                           n_rot, rope_base, eps, q4kv_pos_d,
-                                                           nullptr);
+    qsa_index_score_dk<false><<<gx + extra, 256, 0, q4kv_stream>>>(
+        (uint32_t *)raw_f16, pool, wn_k, k_new, q, wn_q, score, n_head, ratio, n_rot, rope_base,
+        eps, q4kv_pos_d, nullptr, gx, app);
     return q4kv_launch_ok("qsa_index_score_d");
 }
 
@@ -1180,7 +1202,7 @@ extern "C" bool q4_hip_qsa_index_batch(const q4kv_index_desc *d_descs, uint32_t 
     const uint32_t gx = (max_blocks + SC_ROWS_WG - 1) / SC_ROWS_WG;
     qsa_index_score_dk<true><<<dim3(gx, n_items), 256, 0, q4kv_stream>>>(
         nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, n_head, ratio, n_rot,
-        rope_base, eps, nullptr, d_descs);
+        rope_base, eps, nullptr, d_descs, gx, q4kv_app_args{});
     if (max_blocks <= 16u * TK_T)
         qsa_topk_k<TK_BATCH, 16><<<n_items, TK_T, 0, q4kv_stream>>>(
             nullptr, nullptr, 0, k_blk, ratio, 0, width, nullptr, d_descs);

@@ -100,6 +100,64 @@ __device__ static inline void q8_lane_store(uint8_t *blk, uint32_t part, float d
     if (part == 0) *(uint16_t *)blk = __half_as_ushort(__float2half_rn(d));
 }
 
+typedef float q4kv_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t q4kv_u4 __attribute__((ext_vector_type(4)));
+#define QBLK_PER_WG 32u /* 256 threads / 8 lanes per block */
+
+/* Quantise q8_0 blocks [blk0, blk0 + 32) of src into dst (block-indexed) with
+ * one 256-thread workgroup; the 1088 output bytes are assembled in LDS and
+ * written as 16-byte stores where dst allows. */
+__device__ static inline void q8_quant_wg(const float *__restrict__ src,
+                                          uint8_t *__restrict__ dst, uint64_t nblocks,
+                                          uint64_t blk0, bool src_al16, bool dst_al16) {
+    __shared__ __attribute__((aligned(16))) uint8_t ob[QBLK_PER_WG * 34u];
+    const uint32_t t = threadIdx.x, lb = t >> 3, part = t & 7u;
+    const uint64_t b = blk0 + lb;
+    const bool live = b < nblocks;
+    float x0 = 0.f, x1 = 0.f, x2 = 0.f, x3 = 0.f;
+    if (live) {
+        const float *p = src + b * 32u + part * 4u;
+        if (src_al16) {
+            const q4kv_f4 v = ldg((const q4kv_f4 *)p);
+            x0 = v[0]; x1 = v[1]; x2 = v[2]; x3 = v[3];
+        } else {
+            x0 = ldg(p); x1 = ldg(p + 1); x2 = ldg(p + 2); x3 = ldg(p + 3);
+        }
+    }
+    int q[4];
+    const float d = q8_lane_quant(x0, x1, x2, x3, q);
+    q8_lane_store(ob + lb * 34u, part, d, q);
+    __syncthreads();
+    const uint64_t nb = nblocks - blk0 < QBLK_PER_WG ? nblocks - blk0 : QBLK_PER_WG;
+    uint8_t *out = dst + blk0 * 34u;
+    if (dst_al16 && nb == QBLK_PER_WG) {
+        if (t < QBLK_PER_WG * 34u / 16u) stg((q4kv_u4 *)out + t, ((const q4kv_u4 *)ob)[t]);
+    } else {
+        for (uint32_t i = t; i < nb * 34u; i += blockDim.x) stg(out + i, ob[i]);
+    }
+}
+
+/* A held append carried by another launch: workgroups w < wgs of the
+ * carrying range write the K rows, wgs <= w < 2 wgs the V rows, q8_0 at the
+ * device position (n values per cache, 32 blocks per workgroup), as the
+ * append kernel itself would. */
+struct q4kv_app_args {
+    const float *k, *v;
+    uint8_t *kc, *vc;
+    const int32_t *pp;
+    uint32_t n, bpt, wgs;
+};
+__device__ static inline void q4kv_app_wg(const q4kv_app_args &a, uint32_t w) {
+    const bool isv = w >= a.wgs;
+    const float *src = isv ? a.v : a.k;
+    uint8_t *dst = (isv ? a.vc : a.kc) + (size_t)(uint32_t)ldg(a.pp) * a.bpt;
+    q8_quant_wg(src, dst, a.n / 32u, (uint64_t)(isv ? w - a.wgs : w) * QBLK_PER_WG,
+                ((uintptr_t)src & 15u) == 0, ((uintptr_t)dst & 15u) == 0);
+}
+/* Hands the held append (if any) to a launch that carries it and clears the
+ * hold: returns the number of extra workgroups it needs (0: none held). */
+uint32_t q4kv_take_held(q4kv_app_args *a);
+
 /* ---- shared wave-level arithmetic of the Q/K preparation ---- */
 template <int CTRL> __device__ static inline float q4kv_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));

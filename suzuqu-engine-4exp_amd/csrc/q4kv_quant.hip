@@ -23,41 +23,6 @@ extern "C" {
 #include "q4kv.h"
 }
 
-typedef float fv4 __attribute__((ext_vector_type(4)));
-typedef uint32_t uv4 __attribute__((ext_vector_type(4)));
-
-#define QBLK_PER_WG 32u /* 256 threads / 8 lanes per block */
-
-/* Quantise blocks [blk0, blk0+32) of src into dst (block-indexed). */
-__device__ static void q8_quant_wg(const float *__restrict__ src, uint8_t *__restrict__ dst,
-                                   uint64_t nblocks, uint64_t blk0, bool src_al16,
-                                   bool dst_al16) {
-    __shared__ __attribute__((aligned(16))) uint8_t ob[QBLK_PER_WG * 34u];
-    const uint32_t t = threadIdx.x, lb = t >> 3, part = t & 7u;
-    const uint64_t b = blk0 + lb;
-    const bool live = b < nblocks;
-    float x0 = 0.f, x1 = 0.f, x2 = 0.f, x3 = 0.f;
-    if (live) {
-        const float *p = src + b * 32u + part * 4u;
-        if (src_al16) {
-            const fv4 v = ldg((const fv4 *)p);
-            x0 = v[0]; x1 = v[1]; x2 = v[2]; x3 = v[3];
-        } else {
-            x0 = ldg(p); x1 = ldg(p + 1); x2 = ldg(p + 2); x3 = ldg(p + 3);
-        }
-    }
-    int q[4];
-    const float d = q8_lane_quant(x0, x1, x2, x3, q);
-    q8_lane_store(ob + lb * 34u, part, d, q);
-    __syncthreads();
-    const uint64_t nb = nblocks - blk0 < QBLK_PER_WG ? nblocks - blk0 : QBLK_PER_WG;
-    uint8_t *out = dst + blk0 * 34u;
-    if (dst_al16 && nb == QBLK_PER_WG) {
-        if (t < QBLK_PER_WG * 34u / 16u) stg((uv4 *)out + t, ((const uv4 *)ob)[t]);
-    } else {
-        for (uint32_t i = t; i < nb * 34u; i += blockDim.x) stg(out + i, ob[i]);
-    }
-}
 
 __global__ __launch_bounds__(256) static void f32_to_q8_k(const float *__restrict__ src,
                                                           uint8_t *__restrict__ dst,
@@ -228,6 +193,15 @@ bool q4kv_flush(void) {
     q4kv_held.on = 0;
     return append_launch(q4kv_held.kc, q4kv_held.vc, q4kv_held.k, q4kv_held.v, q4kv_held.n,
                          q4kv_held.bpt, q4kv_held.kind);
+}
+
+uint32_t q4kv_take_held(q4kv_app_args *a) {
+    if (!q4kv_held.on) return 0;
+    q4kv_held.on = 0;
+    const uint32_t wgs = (q4kv_held.n / 32u + QBLK_PER_WG - 1) / QBLK_PER_WG;
+    *a = q4kv_app_args{q4kv_held.k,  q4kv_held.v, q4kv_held.kc,  q4kv_held.vc,
+                       q4kv_pos_d,   q4kv_held.n, q4kv_held.bpt, wgs};
+    return 2u * wgs;
 }
 
 /* Q4KV_HOLD_APPEND=0 launches every append at once (no held append). */
