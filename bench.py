@@ -980,7 +980,9 @@ def config_indexer(b, steps=100, layers=12):
     from HBM. Also times the prefill pool rebuild of one layer."""
     rt, lib = b.rt, b.lib
     max_blocks = CTX // IDX_RATIO
-    pos = CTX - 1
+    # a position whose visible blocks (65386) do not fill the top-k's 65536-key
+    # load exactly, as almost every decode position
+    pos = CTX - 601
     raws, pools, scs, sels, qs, ks = [], [], [], [], [], []
     tmp = rt.alloc(CTX * IDX_DIM * 4)
     wn = rt.alloc(IDX_DIM * 4)

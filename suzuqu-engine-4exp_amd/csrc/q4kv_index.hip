@@ -645,15 +645,29 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
      * that key is 0), so the radix passes need no validity test; the
      * compactions check validity where a threshold can be 0. */
     auto load_chunk = [&](uint32_t c) {
-        const float *src = row + (size_t)c * TK_CHUNK + tid;
+        const float *src = row + (size_t)c * TK_CHUNK;
         const uint32_t lim = n_vis - c * TK_CHUNK;
         if (lim >= TK_CHUNK) {
 #pragma unroll
-            for (uint32_t r = 0; r < KPT; r++) key[r] = xkey(ldg(src + r * TK_T));
+            for (uint32_t r = 0; r < KPT; r++) key[r] = xkey(ldg(src + r * TK_T + tid));
         } else {
+            /* a partial chunk through a buffer resource of lim elements:
+             * loads past it return 0 with no branch, so all KPT loads are in
+             * flight together (a load under a per-element branch waits for
+             * itself); those elements then take key 0 */
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)src, (short)0, (int)(lim * 4u), 0x00020000);
 #pragma unroll
             for (uint32_t r = 0; r < KPT; r++)
-                key[r] = r * TK_T + tid < lim ? xkey(ldg(src + r * TK_T)) : 0u;
+                key[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(tid * 4u),
+                                                              (int)(r * TK_T * 4u), 0);
+#pragma unroll
+            for (uint32_t r = 0; r < KPT; r++) {
+                /* the loaded word is used whatever the condition, so the load
+                 * is not moved under it */
+                asm volatile("" : "+v"(key[r]));
+                key[r] = r * TK_T + tid < lim ? xkey(__uint_as_float(key[r])) : 0u;
+            }
         }
     };
     auto valid = [&](uint32_t c, uint32_t r) { return c * TK_CHUNK + r * TK_T + tid < n_vis; };

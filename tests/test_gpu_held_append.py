@@ -252,7 +252,8 @@ def test_held_append_carried_by_the_indexer(rt, oracle, fused):
             layer(d, pos, held)
             outs.append([rt.download(d["kc"], hk.size), rt.download(d["vc"], hv.size),
                          rt.download(d["raw"], raw.nbytes), rt.download(d["pool"], pool0.nbytes),
-                         rt.download(d["sc"], max_blocks * 4), rt.download(d["sel"], WIDTH * 4),
+                         rt.download(d["sc"], (pos + 1) // RATIO * 4),  # rows written
+                         rt.download(d["sel"], WIDTH * 4),
                          rt.download(d["out"], q.nbytes)])
         _append_oracle(oracle, hk, hv, k[pos], v[pos], n, bpt, pos)
         assert np.array_equal(outs[1][0], hk), f"pos {pos}: K cache bytes"
