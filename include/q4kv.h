@@ -65,8 +65,10 @@ bool q4_hip_f32_to_f16(void *dst_f16, const float *src, uint64_t n);
  * caches with bpt bytes per token, width `kind` (src/q4.h:694-695).
  * A q8_0 append of whole 256-dim head rows (bpt = n / 256 * 272) is held,
  * not launched: the next one-token decode over the same caches performs it
- * inside its own launch, and any other q4_hip_* / q4kv_* call launches it
- * first, so every library call sees the appended rows, in stream order.
+ * inside its own launch, as do the indexer calls that follow the append in
+ * the reference's layer (q4_hip_f32_to_f16_d, q4_hip_qsa_index_score_d: extra
+ * workgroups of their launch), and any other q4_hip_* / q4kv_* call launches
+ * it first, so every library call sees the appended rows, in stream order.
  * Work the caller enqueues itself on the stream between this call and the
  * next library call does not (it must not read the caches or overwrite k
  * and v there). Q4KV_HOLD_APPEND=0 launches every append at once. */
