@@ -355,6 +355,18 @@ __device__ static inline void dma16(const void *src, void *lds_wave_base) {
                                      0, 0);
 }
 
+/* 16 bytes global -> LDS like dma16, issued from inline assembly so that the
+ * compiler does not add its own wait for the DMA before every LDS read of
+ * the staging buffers (it cannot tell the two buffers apart); the kernels
+ * that use it wait for their DMAs themselves, with explicit vmcnt counts. */
+__device__ static inline void dma16_manual(const void *src, void *lds_wave_base) {
+    const uint32_t m0 =
+        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(LOCAL void *)lds_wave_base);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0), "v"((const GLOBAL void *)src)
+                 : "memory", "m0");
+}
 /* Reductions over the 16 lanes of a DPP row (one MFMA column group). */
 template <int CTRL> __device__ static inline float dppf(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
@@ -1479,9 +1491,16 @@ __device__ static inline uint32_t lds_u16x2(const uint8_t *a, const uint8_t *b) 
 
 /* APP: the launch also performs a held append of one token's K/V rows at
  * the device position (as the step modes do with a descriptor's rows). */
-template <int MODE, int HG, bool APP = false>
+/* PIPE (prefill: one head group, many passes per wave): the K and V rows of
+ * pass p + 1 are DMA'd while pass p is computed, K behind the P.V products,
+ * V behind the next scores; the waits count the wave's own DMAs (issued from
+ * inline assembly so that the compiler adds no wait of its own before the
+ * LDS reads). */
+template <int MODE, int HG, bool APP = false, bool PIPE = false>
 __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     constexpr bool STEPL = IS_STEP(MODE) || APP; /* a token's rows are appended */
+    static_assert(!PIPE || (HG == 1 && !STEPL && MODE == MODE_INDEXED),
+                  "the pipelined passes are the prefill instance's");
     constexpr uint32_t ROWB = 272, NCH = 17;
     constexpr uint32_t NSLAB = 4u / HG, NE = NSLAB * SLAB; /* slabs, entries per pass */
     constexpr uint32_t RBYTES = 2u * NE * ROWB;           /* K rows | V rows */
@@ -1577,6 +1596,17 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     /* issue pass p: positions into s_pos, the slab's K/V rows by DMA (32 x
      * 17 sixteen-byte pieces per cache, piece u * 64 + lane, row = piece /
      * 17); returns whether the slab holds any valid position */
+    /* PIPE: one cache's rows of the slab (9 DMA instructions per wave) */
+    auto rows_dma = [&](const uint8_t *base, uint8_t *dst, int32_t p) {
+#pragma unroll
+        for (uint32_t u = 0; u < 9u; u++) {
+            const uint32_t e = u * 64u + lane;
+            const uint32_t r = e / NCH, q = e - r * NCH;
+            const int32_t pr = __builtin_amdgcn_ds_bpermute((int)((r & 31u) * 4u), p);
+            const uint64_t off = (uint64_t)(uint32_t)(pr < 0 ? 0 : pr) * rstride32 + q * 16u;
+            if (u < 8u || lane < 32u) dma16_manual(base + off, dst + u * 1024u);
+        }
+    };
     auto issue = [&](uint32_t pass, uint32_t &ne, int32_t &pos) -> bool {
         const uint32_t e0 = j0 + pass * NE + slab * SLAB;
         ne = e0 < j1 ? min(SLAB, j1 - e0) : 0u;
@@ -1584,15 +1614,20 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         const bool any = __ballot(pos >= 0) != 0u;
         if (lane < 32u && hg == 0u) s_pos[slab * SLAB + lane] = pos;
         if (hg == 0u && any) {
+            if constexpr (PIPE) {
+                rows_dma(kbase, krow, pos);
+            } else {
 #pragma unroll
-            for (uint32_t u = 0; u < 9u; u++) {
-                const uint32_t e = u * 64u + lane;
-                const uint32_t r = e / NCH, q = e - r * NCH;
-                const int32_t pr = __builtin_amdgcn_ds_bpermute((int)((r & 31u) * 4u), pos);
-                const uint64_t off = (uint64_t)(uint32_t)(pr < 0 ? 0 : pr) * rstride32 + q * 16u;
-                if (u < 8u || lane < 32u) {
-                    dma16(kbase + off, krow + u * 1024u);
-                    dma16(vbase + off, vrow + u * 1024u);
+                for (uint32_t u = 0; u < 9u; u++) {
+                    const uint32_t e = u * 64u + lane;
+                    const uint32_t r = e / NCH, q = e - r * NCH;
+                    const int32_t pr = __builtin_amdgcn_ds_bpermute((int)((r & 31u) * 4u), pos);
+                    const uint64_t off =
+                        (uint64_t)(uint32_t)(pr < 0 ? 0 : pr) * rstride32 + q * 16u;
+                    if (u < 8u || lane < 32u) {
+                        dma16(kbase + off, krow + u * 1024u);
+                        dma16(vbase + off, vrow + u * 1024u);
+                    }
                 }
             }
         }
@@ -1601,6 +1636,16 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     uint32_t ne = 0;
     int32_t pos = -1;
     bool any = n_pass > 0u ? issue(0u, ne, pos) : false;
+    if constexpr (PIPE) {
+        /* pass 0's V rows, then pass 1's list entries: one load always (a
+         * repeat of entry j0 past the split), so the DMA waits below count
+         * exactly */
+        if (n_pass > 0u && any) rows_dma(vbase, vrow, pos);
+        if (n_pass > 0u) {
+            const uint32_t e = j0 + NE + slab * SLAB + (lane & 31u);
+            raw = ldg(it.list + (e < j1 ? e : j0));
+        }
+    }
     TRACEW(1);
 
     if (PREP) {
@@ -1670,168 +1715,216 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     const float qmul = s_qm[8u * hg + (c & 7u)]; /* this lane's column's head */
     const h8_t k_bias = (h8_t)((_Float16)1152.0f);
 
-    for (uint32_t pass = 0; pass < n_pass; pass++) {
-        if (pass > 0u) any = issue(pass, ne, pos);
-        /* the next pass's list entries (a wave rarely has more than one) */
-        raw = -1;
-        {
-            const uint32_t e = j0 + (pass + 1u) * NE + slab * SLAB + (lane & 31u);
-            if (pass + 1u < n_pass && e < j1) raw = it.list ? ldg(it.list + e) : (int32_t)e;
-        }
-        __builtin_amdgcn_s_waitcnt(0);
-        TRACEW(3);
-        if (HG > 1) __syncthreads(); /* the head-group waves share the slab's rows */
-        if (hg == 0u && any) {
-            if (STEPL) {
-                /* rows at the appended position take the new token's bytes */
-                uint64_t hit = __ballot(lane < 32u && pos >= 0 && (uint32_t)pos == it.pos_new);
-                if (hit) {
-                    int q[4], qv[4];
-                    const float dk = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
-                    const float dv = q8_lane_quant(nv[0], nv[1], nv[2], nv[3], qv);
-                    while (hit) {
-                        const uint32_t r = __builtin_ctzll(hit);
-                        hit &= hit - 1u;
-                        q8_lane_store(krow + r * ROWB + 34u * (lane >> 3), lane & 7u, dk, q);
-                        q8_lane_store(vrow + r * ROWB + 34u * (lane >> 3), lane & 7u, dv, qv);
-                    }
-                }
-            }
-            /* padding rows (never fetched, or fetched from row 0): zero their
-             * K block scales; the V block scales go block-major to vsT, 0 at
-             * padding */
-            if (lane < 32u && pos < 0) {
+    /* pass bodies shared by both loops: the scores and softmax of the slab
+     * (P, m_run, l_run, the rescaled acc), then its P.V products */
+    float P[8];
+    auto scores_softmax = [&](uint32_t pass) {
+        TRACEW(4);
+        /* ---- scores: two 16-position tiles ---- */
+        f4_t S[2];
 #pragma unroll
-                for (uint32_t b = 0; b < 8u; b++) *(uint16_t *)(krow + lane * ROWB + 34u * b) = 0;
-            }
-            {
-                const uint32_t p = lane & 31u;
-                const bool valid = s_pos[slab * SLAB + p] >= 0;
-#pragma unroll
-                for (uint32_t k = 0; k < 4u; k++) {
-                    const uint32_t b = (lane >> 5) + 2u * k;
-                    vsT[slab][b][p] = valid ? *(const uint16_t *)(vrow + p * ROWB + 34u * b) : 0;
-                }
-            }
+        for (uint32_t t = 0; t < 2u; t++) {
+            /* this lane's rows 4 jg .. 4 jg + 3 of tile t: padding rows
+             * start at -inf (their K scales are zero and their bytes
+             * finite, so they stay there; a pass that is computed holds a
+             * valid row, so the maximum is finite) */
+            const int4 ps = *(const int4 *)&s_pos[slab * SLAB + 16u * t + 4u * jg];
+            S[t] = (f4_t){ps.x < 0 ? -INFINITY : 0.f, ps.y < 0 ? -INFINITY : 0.f,
+                          ps.z < 0 ? -INFINITY : 0.f, ps.w < 0 ? -INFINITY : 0.f};
         }
-        if (HG > 1) __syncthreads();
-        if (any) {
-            TRACEW(4);
-            /* ---- scores: two 16-position tiles ---- */
-            f4_t S[2];
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++) {
+            const h8_t qb = *(const h8_t *)(qBw + b * 4u * 16u * 8u);
 #pragma unroll
             for (uint32_t t = 0; t < 2u; t++) {
-                /* this lane's rows 4 jg .. 4 jg + 3 of tile t: padding rows
-                 * start at -inf (their K scales are zero and their bytes
-                 * finite, so they stay there; a pass that is computed holds a
-                 * valid row, so the maximum is finite) */
-                const int4 ps = *(const int4 *)&s_pos[slab * SLAB + 16u * t + 4u * jg];
-                S[t] = (f4_t){ps.x < 0 ? -INFINITY : 0.f, ps.y < 0 ? -INFINITY : 0.f,
-                              ps.z < 0 ? -INFINITY : 0.f, ps.w < 0 ? -INFINITY : 0.f};
-            }
+                /* exact k: the products need no bias correction, so their
+                 * sum rounds at the size of q.k whatever |q| */
+                const h8_t kb =
+                    k_operand_biased(krow + (16u * t + c) * ROWB, b, jg, k_eoff, k_esel) -
+                    k_bias;
+                const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    kb, qb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const uint8_t *rs = krow + (16u * t + 4u * jg) * ROWB + 34u * b;
 #pragma unroll
-            for (uint32_t b = 0; b < 8u; b++) {
-                const h8_t qb = *(const h8_t *)(qBw + b * 4u * 16u * 8u);
-#pragma unroll
-                for (uint32_t t = 0; t < 2u; t++) {
-                    /* exact k: the products need no bias correction, so their
-                     * sum rounds at the size of q.k whatever |q| */
-                    const h8_t kb =
-                        k_operand_biased(krow + (16u * t + c) * ROWB, b, jg, k_eoff, k_esel) -
-                        k_bias;
-                    const f4_t C = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        kb, qb, (f4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    const uint8_t *rs = krow + (16u * t + 4u * jg) * ROWB + 34u * b;
-#pragma unroll
-                    for (uint32_t i = 0; i < 4u; i++)
-                        S[t][i] = __builtin_fmaf(ld_h(rs + i * ROWB), C[i], S[t][i]);
-                }
-            }
-            TRACEW(5);
-            /* ---- softmax over the slab (base 2; scores already scaled) ---- */
-            float T[8];
-#pragma unroll
-            for (uint32_t i = 0; i < 4u; i++) {
-                T[i] = add_ror8(S[0][i]) * qmul;
-                T[4u + i] = add_ror8(S[1][i]) * qmul;
-            }
-            float mx = fmax3v(fmax3v(T[0], T[1], T[2]), fmax3v(T[3], T[4], T[5]), fmax2(T[6], T[7]));
-            mx = max32(max16(mx));
-            const float mn = fmax2(m_run, mx);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
-            const bool grew = mn > m_run;
-            m_run = mn;
-            float P[8], ls = 0.f;
-#pragma unroll
-            for (uint32_t i = 0; i < 8u; i++) {
-                P[i] = __builtin_amdgcn_exp2f(T[i] - mn);
-                ls += P[i];
-            }
-            l_run = l_run * alpha + ls;
-            /* later passes: rescale only when some column's maximum grew
-             * (alpha is 1 elsewhere) */
-            if (pass > 0u && __ballot(grew) != 0u) {
-#pragma unroll
-                for (uint32_t t = 0; t < 16u; t++) acc[t] *= alpha;
-            }
-            TRACEW(6);
-            /* ---- P.V over the 8 blocks: tiles 2b (even dims), 2b + 1 (odd) ---- */
-            /* this lane's 8 positions: 4 jg .. 4 jg + 3, 16 + 4 jg .. 16 + 4 jg + 3 */
-            const uint8_t *vp0 = vrow + (4u * jg) * ROWB, *vp1 = vrow + (16u + 4u * jg) * ROWB;
-            /* block b's LDS operands: V scales of the lane's 8 positions, and
-             * the 16-bit V reads (dims 2c, 2c + 1) at those positions; block
-             * b + 1's are requested before block b is computed */
-            struct VOps {
-                uint32_t vw[4], x[8];
-            };
-            auto load_v = [&](uint32_t b, VOps &o) {
-                const uint2 va = *(const uint2 *)&vsT[slab][b][4u * jg];
-                const uint2 vb = *(const uint2 *)&vsT[slab][b][16u + 4u * jg];
-                o.vw[0] = va.x;
-                o.vw[1] = va.y;
-                o.vw[2] = vb.x;
-                o.vw[3] = vb.y;
-                const uint8_t *s0 = vp0 + 34u * b + 2u + 2u * c, *s1 = vp1 + 34u * b + 2u + 2u * c;
-#pragma unroll
-                for (uint32_t i = 0; i < 8u; i++)
-                    o.x[i] = *(const uint16_t *)((i < 4u ? s0 : s1) + (i & 3u) * ROWB);
-            };
-            VOps cur, nxt;
-            load_v(0u, cur);
-#pragma unroll
-            for (uint32_t b = 0; b < 8u; b++) {
-                if (b + 1u < 8u) load_v(b + 1u, nxt);
-                __builtin_amdgcn_sched_barrier(0);
-                float u[8];
-#pragma unroll
-                for (uint32_t i = 0; i < 4u; i++) {
-                    u[2u * i] = __builtin_fmaf(P[2u * i], h2lo(cur.vw[i]), 0.f);
-                    u[2u * i + 1u] = __builtin_fmaf(P[2u * i + 1u], h2hi(cur.vw[i]), 0.f);
-                }
-                const u4_t bw = {split_pk(u[0], u[1], nsel), split_pk(u[2], u[3], nsel),
-                                 split_pk(u[4], u[5], nsel), split_pk(u[6], u[7], nsel)};
-                const h8_t B = __builtin_bit_cast(h8_t, bw);
-                /* V^T: each 16-bit read holds dims 2c, 2c + 1 of one position;
-                 * two positions' even (odd) bytes go to one fp16 pair, which
-                 * the xor turns into 1024 + (b ^ 0x80) = 1152 + b */
-                u4_t E, O;
-#pragma unroll
-                for (uint32_t k = 0; k < 4u; k++) {
-                    E[k] = __builtin_amdgcn_perm(cur.x[2u * k + 1u], cur.x[2u * k], 0x0C040C00u) ^ 0x64806480u;
-                    O[k] = __builtin_amdgcn_perm(cur.x[2u * k + 1u], cur.x[2u * k], 0x0C050C01u) ^ 0x64806480u;
-                }
-                acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(h8_t, E), B, acc[2u * b], 0, 0, 0);
-                acc[2u * b + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(h8_t, O), B, acc[2u * b + 1u], 0, 0, 0);
-                acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b], 0, 0, 0);
-                acc[2u * b + 1u] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b + 1u], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                cur = nxt;
+                for (uint32_t i = 0; i < 4u; i++)
+                    S[t][i] = __builtin_fmaf(ld_h(rs + i * ROWB), C[i], S[t][i]);
             }
         }
-        if (HG > 1) __syncthreads(); /* the slab's rows are refilled next pass */
+        TRACEW(5);
+        /* ---- softmax over the slab (base 2; scores already scaled) ---- */
+        float T[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; i++) {
+            T[i] = add_ror8(S[0][i]) * qmul;
+            T[4u + i] = add_ror8(S[1][i]) * qmul;
+        }
+        float mx = fmax3v(fmax3v(T[0], T[1], T[2]), fmax3v(T[3], T[4], T[5]), fmax2(T[6], T[7]));
+        mx = max32(max16(mx));
+        const float mn = fmax2(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - mn);
+        const bool grew = mn > m_run;
+        m_run = mn;
+        float ls = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; i++) {
+            P[i] = __builtin_amdgcn_exp2f(T[i] - mn);
+            ls += P[i];
+        }
+        l_run = l_run * alpha + ls;
+        /* later passes: rescale only when some column's maximum grew
+         * (alpha is 1 elsewhere) */
+        if (pass > 0u && __ballot(grew) != 0u) {
+#pragma unroll
+            for (uint32_t t = 0; t < 16u; t++) acc[t] *= alpha;
+        }
+        TRACEW(6);
+    };
+    auto pv = [&]() {
+        /* ---- P.V over the 8 blocks: tiles 2b (even dims), 2b + 1 (odd) ---- */
+        /* this lane's 8 positions: 4 jg .. 4 jg + 3, 16 + 4 jg .. 16 + 4 jg + 3 */
+        const uint8_t *vp0 = vrow + (4u * jg) * ROWB, *vp1 = vrow + (16u + 4u * jg) * ROWB;
+        /* block b's LDS operands: V scales of the lane's 8 positions, and
+         * the 16-bit V reads (dims 2c, 2c + 1) at those positions; block
+         * b + 1's are requested before block b is computed */
+        struct VOps {
+            uint32_t vw[4], x[8];
+        };
+        auto load_v = [&](uint32_t b, VOps &o) {
+            const uint2 va = *(const uint2 *)&vsT[slab][b][4u * jg];
+            const uint2 vb = *(const uint2 *)&vsT[slab][b][16u + 4u * jg];
+            o.vw[0] = va.x;
+            o.vw[1] = va.y;
+            o.vw[2] = vb.x;
+            o.vw[3] = vb.y;
+            const uint8_t *s0 = vp0 + 34u * b + 2u + 2u * c, *s1 = vp1 + 34u * b + 2u + 2u * c;
+#pragma unroll
+            for (uint32_t i = 0; i < 8u; i++)
+                o.x[i] = *(const uint16_t *)((i < 4u ? s0 : s1) + (i & 3u) * ROWB);
+        };
+        VOps cur, nxt;
+        load_v(0u, cur);
+#pragma unroll
+        for (uint32_t b = 0; b < 8u; b++) {
+            if (b + 1u < 8u) load_v(b + 1u, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            float u[8];
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; i++) {
+                u[2u * i] = __builtin_fmaf(P[2u * i], h2lo(cur.vw[i]), 0.f);
+                u[2u * i + 1u] = __builtin_fmaf(P[2u * i + 1u], h2hi(cur.vw[i]), 0.f);
+            }
+            const u4_t bw = {split_pk(u[0], u[1], nsel), split_pk(u[2], u[3], nsel),
+                             split_pk(u[4], u[5], nsel), split_pk(u[6], u[7], nsel)};
+            const h8_t B = __builtin_bit_cast(h8_t, bw);
+            /* V^T: each 16-bit read holds dims 2c, 2c + 1 of one position;
+             * two positions' even (odd) bytes go to one fp16 pair, which
+             * the xor turns into 1024 + (b ^ 0x80) = 1152 + b */
+            u4_t E, O;
+#pragma unroll
+            for (uint32_t k = 0; k < 4u; k++) {
+                E[k] = __builtin_amdgcn_perm(cur.x[2u * k + 1u], cur.x[2u * k], 0x0C040C00u) ^ 0x64806480u;
+                O[k] = __builtin_amdgcn_perm(cur.x[2u * k + 1u], cur.x[2u * k], 0x0C050C01u) ^ 0x64806480u;
+            }
+            acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(h8_t, E), B, acc[2u * b], 0, 0, 0);
+            acc[2u * b + 1u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                __builtin_bit_cast(h8_t, O), B, acc[2u * b + 1u], 0, 0, 0);
+            acc[2u * b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b], 0, 0, 0);
+            acc[2u * b + 1u] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(neg, B, acc[2u * b + 1u], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            cur = nxt;
+        }
+    };
+    /* padding rows (never fetched, or fetched from row 0): zero their K block
+     * scales */
+    auto k_fix = [&]() {
+        if (lane < 32u && pos < 0) {
+#pragma unroll
+            for (uint32_t b = 0; b < 8u; b++) *(uint16_t *)(krow + lane * ROWB + 34u * b) = 0;
+        }
+    };
+    /* the V block scales go block-major to vsT, 0 at padding */
+    auto v_fix = [&]() {
+        const uint32_t p = lane & 31u;
+        const bool valid = s_pos[slab * SLAB + p] >= 0;
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; k++) {
+            const uint32_t b = (lane >> 5) + 2u * k;
+            vsT[slab][b][p] = valid ? *(const uint16_t *)(vrow + p * ROWB + 34u * b) : 0;
+        }
+    };
+
+    if constexpr (PIPE) {
+        for (uint32_t pass = 0; pass < n_pass; pass++) {
+            /* pass p's K rows have landed when at most its V rows (9 DMA
+             * instructions) and the next list load are outstanding */
+            if (any) {
+                __builtin_amdgcn_s_waitcnt(0x0F7A); /* vmcnt(10) */
+                TRACEW(3);
+                k_fix();
+                scores_softmax(pass);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): V rows, the list load */
+            /* the list word is consumed here on every path, so the compiler
+             * has no load of its own pending later (its wait would also
+             * drain the next pass's DMA) */
+            asm volatile("" ::"v"(raw));
+            if (any) v_fix();
+            /* pass p + 1: its K rows behind this pass's P.V, its V rows behind
+             * its own scores, then pass p + 2's list entries (one load always) */
+            uint32_t ne_n = 0;
+            int32_t pos_n = -1;
+            const bool any_n = pass + 1u < n_pass ? issue(pass + 1u, ne_n, pos_n) : false;
+            if (any) pv();
+            if (any_n) rows_dma(vbase, vrow, pos_n);
+            {
+                const uint32_t e = j0 + (pass + 2u) * NE + slab * SLAB + (lane & 31u);
+                raw = ldg(it.list + (e < j1 ? e : j0));
+            }
+            any = any_n;
+            pos = pos_n;
+            ne = ne_n;
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* the last (unused) list load */
+    } else {
+        for (uint32_t pass = 0; pass < n_pass; pass++) {
+            if (pass > 0u) any = issue(pass, ne, pos);
+            /* the next pass's list entries (a wave rarely has more than one) */
+            raw = -1;
+            {
+                const uint32_t e = j0 + (pass + 1u) * NE + slab * SLAB + (lane & 31u);
+                if (pass + 1u < n_pass && e < j1) raw = it.list ? ldg(it.list + e) : (int32_t)e;
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            TRACEW(3);
+            if (HG > 1) __syncthreads(); /* the head-group waves share the slab's rows */
+            if (hg == 0u && any) {
+                if (STEPL) {
+                    /* rows at the appended position take the new token's bytes */
+                    uint64_t hit = __ballot(lane < 32u && pos >= 0 && (uint32_t)pos == it.pos_new);
+                    if (hit) {
+                        int q[4], qv[4];
+                        const float dk = q8_lane_quant(nk[0], nk[1], nk[2], nk[3], q);
+                        const float dv = q8_lane_quant(nv[0], nv[1], nv[2], nv[3], qv);
+                        while (hit) {
+                            const uint32_t r = __builtin_ctzll(hit);
+                            hit &= hit - 1u;
+                            q8_lane_store(krow + r * ROWB + 34u * (lane >> 3), lane & 7u, dk, q);
+                            q8_lane_store(vrow + r * ROWB + 34u * (lane >> 3), lane & 7u, dv, qv);
+                        }
+                    }
+                }
+                k_fix();
+                v_fix();
+            }
+            if (HG > 1) __syncthreads();
+            if (any) {
+                scores_softmax(pass);
+                pv();
+            }
+            if (HG > 1) __syncthreads(); /* the slab's rows are refilled next pass */
+        }
     }
     TRACEW(7);
 
@@ -1945,6 +2038,16 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 constexpr uint32_t H16_SL = 16;  /* list entries per slab */
+
+/* Q4KV_SLAB_PIPE=0 keeps the prefill slab passes unpipelined. */
+static bool slab_pipe_enabled(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_SLAB_PIPE");
+        v = (e && e[0] == '0') ? 0 : 1;
+    }
+    return v != 0;
+}
 
 static bool h16_enabled(void) {
     static int v = -1;
@@ -2451,18 +2554,6 @@ constexpr uint32_t BAND_MIN = 64;               /* shortest run worth a band */
 constexpr uint32_t BAND_SPAN = 1024;            /* widest union of a workgroup's bands */
 constexpr uint32_t BP = 32;                     /* positions per pass */
 
-/* 16 bytes global -> LDS like dma16, issued from inline assembly so that the
- * compiler does not add its own wait for the DMA before every LDS read of
- * the staging buffers (it cannot tell the two buffers apart); the band
- * kernel waits for its DMAs itself, with explicit vmcnt counts. */
-__device__ static inline void dma16_manual(const void *src, void *lds_wave_base) {
-    const uint32_t m0 =
-        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(LOCAL void *)lds_wave_base);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(m0), "v"((const GLOBAL void *)src)
-                 : "memory", "m0");
-}
 /* workgroup barrier that waits for this wave's LDS accesses only (the
  * __syncthreads fence also drains every outstanding global load, including
  * the next pass's DMA) */
@@ -3564,8 +3655,17 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
                 else
                     qsa_slab_k<MODE, 2, true><<<grid, 256, 0, q4kv_stream>>>(a);
             }
-        } else if (pl.slab && pl.hg == 1u)
-            qsa_slab_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
+        } else if (pl.slab && pl.hg == 1u) {
+            bool piped = false;
+            if constexpr (MODE == MODE_INDEXED) {
+                /* prefill-sized splits: the pipelined passes */
+                if (S == 1u && a.idx && slab_pipe_enabled()) {
+                    qsa_slab_k<MODE, 1, false, true><<<grid, 256, 0, q4kv_stream>>>(a);
+                    piped = true;
+                }
+            }
+            if (!piped) qsa_slab_k<MODE, 1><<<grid, 256, 0, q4kv_stream>>>(a);
+        }
         else if (pl.slab)
             qsa_slab_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (fast && cps >= db_min_chunks())
