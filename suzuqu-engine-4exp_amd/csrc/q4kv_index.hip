@@ -418,12 +418,35 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
         blk = blk < n_blocks ? blk : n_blocks - 1;
         bp[b] = pool + (size_t)blk * IDX_HD + 8u * kq;
     }
+    /* every A load is issued (ap points at a real row for any lane) and
+     * padding lanes are zeroed by a mask afterwards: a load under the lane's
+     * condition would wait for itself. The first k-step's B rows are
+     * requested in the same round trip. */
+    float4 xa[4][2], yb[2][4][2];
 #pragma unroll
     for (int a = 0; a < 4; a++) {
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 x0 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * wave)) : z;
-        const float4 x1 = av[a] ? ld_vec((const float4 *)(ap[a] + 32u * wave) + 1) : z;
-        split_bf16(x0, x1, a_hi[wave][a][lane], a_lo[wave][a][lane]);
+        xa[a][0] = ld_vec((const float4 *)(ap[a] + 32u * wave));
+        xa[a][1] = ld_vec((const float4 *)(ap[a] + 32u * wave) + 1);
+    }
+    auto load_b = [&](uint32_t st, float4 (&y)[4][2]) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            y[b][0] = ld_vec((const float4 *)(bp[b] + 32u * st));
+            y[b][1] = ld_vec((const float4 *)(bp[b] + 32u * st) + 1);
+        }
+    };
+    load_b(0u, yb[0]);
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const uint32_t m = av[a] ? ~0u : 0u;
+        float4 x[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            x[h] = make_float4(__uint_as_float(__float_as_uint(xa[a][h].x) & m),
+                               __uint_as_float(__float_as_uint(xa[a][h].y) & m),
+                               __uint_as_float(__float_as_uint(xa[a][h].z) & m),
+                               __uint_as_float(__float_as_uint(xa[a][h].w) & m));
+        split_bf16(x[0], x[1], a_hi[wave][a][lane], a_lo[wave][a][lane]);
     }
     __syncthreads();
     if (blk0 >= n_blocks) return;
@@ -441,12 +464,9 @@ __global__ __launch_bounds__(256) void qsa_score_mfma_k(const float *q, const fl
             Ah[a] = a_hi[st][a][lane];
             Al[a] = a_lo[st][a][lane];
         }
+        if (st + 1u < 4u) load_b(st + 1u, yb[(st + 1u) & 1u]);
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const float4 y0 = ld_vec((const float4 *)(bp[b] + 32u * st));
-            const float4 y1 = ld_vec((const float4 *)(bp[b] + 32u * st) + 1);
-            split_bf16(y0, y1, Bh[b], Bl[b]);
-        }
+        for (int b = 0; b < 4; b++) split_bf16(yb[st & 1u][b][0], yb[st & 1u][b][1], Bh[b], Bl[b]);
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
