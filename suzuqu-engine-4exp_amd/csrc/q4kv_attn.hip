@@ -966,9 +966,17 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
      * are then uniform without a readfirstlane per row DMA */
     const uint32_t tid = threadIdx.x, lane = tid & 63u,
                    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t gqa = a.n_head / a.n_kvh;
+    /* query heads h0 .. h0 + gqa - 1 of the KV head: blockIdx.z is the group
+     * of 8 (9-16 heads per KV head run as two groups over the same rows) */
+    const uint32_t gqa_all = a.n_head / a.n_kvh, h0 = 8u * blockIdx.z;
+    const uint32_t gqa = gqa_all - h0 < 8u ? gqa_all - h0 : 8u;
     const uint32_t kh = item % a.n_kvh;
     Item it = resolve_item<MODE>(a, item);
+    if (h0) {
+        it.q += (size_t)h0 * (MODE == MODE_PSTEP ? 512u : 256u);
+        it.out += (size_t)h0 * 256u;
+        if (it.gate) it.gate += (size_t)h0 * 256u;
+    }
     if (APP) {
         it.knew = a.app_k + (size_t)kh * 256u;
         it.vnew = a.app_v + (size_t)kh * 256u;
@@ -1373,7 +1381,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
             }
         }
     } else {
-        float *pbase = a.part + ((size_t)item * a.S + s) * gqa * PSTRIDE;
+        float *pbase = a.part + (((size_t)item * a.S + s) * gqa_all + h0) * PSTRIDE;
 #pragma unroll
         for (uint32_t k = 0; k < 2u; k++) {
             const uint32_t e = tid + 256u * k, h = e >> 6, c4 = (e & 63u) * 4u;
@@ -1392,7 +1400,7 @@ __global__ __launch_bounds__(256, 2) void qsa_q8d256_k(AttnArgs a) {
     /* MODE_STEP: split 0 writes the quantised rows last, so no wait inside
      * the kernel covers these stores (the chunks that list the position
      * took the same bytes in LDS) */
-    const bool writer = s == 0u && (!APP || item < a.n_kvh);
+    const bool writer = s == 0u && h0 == 0u && (!APP || item < a.n_kvh);
     if (STEPL && writer && (APP || it.pos_new < it.max_kv) && step_lane) {
         int nq[4];
         const float nd = q8_lane_quant(nx[0], nx[1], nx[2], nx[3], nq);
@@ -3413,7 +3421,8 @@ static bool launch_any(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t gq
 /* Which kernel runs a launch, and its split division. */
 struct Plan {
     bool slab;    /* qsa_slab_k (else qsa_q8d256_k / qsa_attn_k) */
-    uint32_t hg;  /* slab kernels: head groups of 8 */
+    uint32_t hg;  /* slab kernels: head groups of 8; the chunk kernel: its
+                   * grid.z groups of 8 query heads (2 for 9-16 heads) */
     uint32_t S, cps;
     bool h16;     /* qsa_h16_k (f16 cache, hd 256) */
     bool f32w;    /* qsa_f32w_k (f32 cache, hd 256) */
@@ -3440,6 +3449,21 @@ static int slab_mode(void) {
 static bool slab_takes(uint32_t gqa, bool prefill_sized) {
     const int m = slab_mode();
     return gqa <= 16u && (m == 2 || (m == 1 && (gqa > 8u || prefill_sized)));
+}
+
+/* Launches of up to this many items with 9-16 query heads per KV head take
+ * the chunk kernel in two head groups (Q4KV_CHUNK_HG=<n> sets it, 0 off).
+ * Measured against the slab kernel at 12 and 16 heads per KV head, 262144-
+ * token cache: 9.9 vs 12.0 us at 2 items, 14.6 vs 15.2 at 8, 19.3 vs 19.6
+ * at 16. */
+static uint32_t chunk_hg_max_items(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_CHUNK_HG");
+        v = e ? atoi(e) : 16;
+        if (v < 0) v = 0;
+    }
+    return (uint32_t)v;
 }
 
 template <int KIND, int MODE>
@@ -3479,6 +3503,19 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
     const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
     const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
     const bool prefill_sized = (uint64_t)n_items * s_full > SLAB_MAX_WG;
+    if (KIND == Q4KV_Q8 && hd == 256u && gqa > 8u && gqa <= 16u && !IS_STEP(MODE) &&
+        !IS_BATCH(MODE) && n_items <= chunk_hg_max_items()) {
+        /* a few decode items with 9-16 query heads per KV head: the chunk
+         * kernel in two head groups (grid.z) over the same rows; its shorter
+         * per-workgroup chain beats the slab kernel where latency, not the
+         * doubled gather, bounds the launch */
+        constexpr uint32_t CP = KCfg<KIND>::CP;
+        /* 2 n_items workgroups per split, ceil(gqa / 2) heads' partials each */
+        choose_split(2u * n_items, (max_n + CP - 1u) / CP, (gqa + 1u) / 2u, have_part, cap,
+                     pl.S, pl.cps);
+        pl.hg = 2u;
+        return pl;
+    }
     bool slab = KIND == Q4KV_Q8 && hd == 256u && rows16 && slab_takes(gqa, prefill_sized);
     if (!slab && KIND == Q4KV_Q8 && hd == 256u && rows16 && gqa <= 8u && slab_mode() == 1) {
         /* many items (batched decode): where the chunk kernel would walk
@@ -3579,6 +3616,10 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         plan_launch<KIND, MODE>(a.hd, n_items, max_n, gqa, pb.ptr != nullptr, pb.cap, rows16);
     if (IS_STEP(MODE) && !fast && !pl.slab && !pl.h16 && !pl.f32w) return false; /* the fused append needs these */
     const uint32_t S = pl.S, cps = pl.cps;
+    /* the chunk kernel: up to 8 query heads per KV head, or 9-16 in two
+     * head groups (grid.z) */
+    const uint32_t zg = !pl.slab && !pl.h16 && !pl.f32w && pl.hg == 2u ? 2u : 1u;
+    const bool chunk = fast || zg == 2u;
     if (S > 1u && (!pb.ptr || (size_t)n_items * S * gqa * PSTRIDE > pb.cap)) {
         Q4KV_ERR("qsa attention: %u splits of %u items exceed the partial buffer", S, n_items);
         return false;
@@ -3592,7 +3633,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
          * decode-sized launches (prefill-sized ones run the band kernel
          * first, which reads the rows without the substitution) */
         app = a.hd == 256u && n_items <= 64u && held_matches(a) &&
-              ((fast && !pl.slab && cps < db_min_chunks()) ||
+              ((chunk && !pl.slab && cps < db_min_chunks()) ||
                (pl.slab && gqa <= 16u && !(S == 1u && gqa <= 8u)));
         if (app) {
             a.app_k = q4kv_held.k;
@@ -3608,16 +3649,16 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
     for (uint32_t i0 = 0; i0 < n_items; i0 += Q4KV_MAX_GRID_Y) {
         const uint32_t ni = n_items - i0 < Q4KV_MAX_GRID_Y ? n_items - i0 : Q4KV_MAX_GRID_Y;
         a.item0 = i0;
-        dim3 grid(S, ni);
+        dim3 grid(S, ni, zg);
         /* the chunk kernel and the batched slab decode over whole tokens: the
          * KV heads of each (token, split) on one XCD (for the slab kernel's
          * prefill and the f16 / f32 kernels it measured 1-2 % slower) */
         a.xgrp = 0u;
-        const bool grouped = pl.slab ? IS_BATCH(MODE) : (fast && !pl.h16 && !pl.f32w);
+        const bool grouped = pl.slab ? IS_BATCH(MODE) : (chunk && !pl.h16 && !pl.f32w);
         if (grouped && xcd_pair_enabled() && a.n_kvh > 1u && ni == n_items &&
             ni % a.n_kvh == 0u) {
             a.xgrp = ni / a.n_kvh * S;
-            grid = dim3(8u * a.n_kvh * ((a.xgrp + 7u) / 8u), 1u);
+            grid = dim3(8u * a.n_kvh * ((a.xgrp + 7u) / 8u), 1u, zg);
         }
         const bool prof = prof_armed();
         if (prof) (void)hipEventRecord(g_pev[2 * g_prof_n], q4kv_stream);
@@ -3668,12 +3709,12 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
         }
         else if (pl.slab)
             qsa_slab_k<MODE, 2><<<grid, 256, 0, q4kv_stream>>>(a);
-        else if (fast && cps >= db_min_chunks())
+        else if (chunk && cps >= db_min_chunks())
             qsa_q8d256_k<MODE, true><<<grid, 256, 0, q4kv_stream>>>(a);
-        else if (fast && app) {
+        else if (chunk && app) {
             if constexpr (MODE == MODE_INDEXED || MODE == MODE_DENSE)
                 qsa_q8d256_k<MODE, false, true><<<grid, 256, 0, q4kv_stream>>>(a);
-        } else if (fast)
+        } else if (chunk)
             qsa_q8d256_k<MODE, false><<<grid, 256, 0, q4kv_stream>>>(a);
         else if (IS_STEP(MODE))
             return false;
@@ -3689,7 +3730,7 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
             qsa_comb_k<KIND, MODE><<<dim3(gqa, ni), 256, 0, q4kv_stream>>>(a);
     }
     if (op) {
-        if (!fast && !pl.slab) return false;
+        if (!chunk && !pl.slab) return false;
         a.item0 = 0;
         const uint32_t n_rb = (op->n_embd + OUT_RPB - 1u) / OUT_RPB;
         qsa_comb_gemv_k<MODE><<<dim3(a.n_head * n_rb, n_items / a.n_kvh), 256, 0, q4kv_stream>>>(
