@@ -1492,10 +1492,6 @@ __device__ static inline uint32_t split_pk(float x, float y, float nsel) {
 __device__ static inline float ld_h(const uint8_t *p) {
     return (float)__builtin_bit_cast(_Float16, *(const uint16_t *)p);
 }
-/* two 16-bit LDS values packed into one word */
-__device__ static inline uint32_t lds_u16x2(const uint8_t *a, const uint8_t *b) {
-    return (uint32_t)*(const uint16_t *)a | ((uint32_t)*(const uint16_t *)b << 16);
-}
 
 /* APP: the launch also performs a held append of one token's K/V rows at
  * the device position (as the step modes do with a descriptor's rows). */
