@@ -683,10 +683,12 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                                                               (int)(r * TK_T * 4u), 0);
 #pragma unroll
             for (uint32_t r = 0; r < KPT; r++) {
-                /* the loaded word is used whatever the condition, so the load
-                 * is not moved under it */
-                asm volatile("" : "+v"(key[r]));
-                key[r] = r * TK_T + tid < lim ? xkey(__uint_as_float(key[r])) : 0u;
+                /* xkey with its sign-bit term only where the element is in
+                 * the row: past it the word loaded is 0 and its key then 0,
+                 * with no select (which would move the load under it) */
+                const uint32_t u = key[r];
+                const uint32_t in = (r * TK_T + tid - lim) & 0x80000000u;
+                key[r] = u ^ ((uint32_t)((int32_t)u >> 31) | in);
             }
         }
     };
