@@ -3499,12 +3499,15 @@ static Plan plan_launch(uint32_t hd, uint32_t n_items, uint32_t max_n, uint32_t 
     const uint32_t hg = gqa > 8u ? 2u : 1u, ne = 128u / hg;
     const uint32_t s_full = max_n ? (max_n + ne - 1u) / ne : 1u;
     const bool prefill_sized = (uint64_t)n_items * s_full > SLAB_MAX_WG;
-    if (KIND == Q4KV_Q8 && hd == 256u && gqa > 8u && gqa <= 16u && !IS_STEP(MODE) &&
-        !IS_BATCH(MODE) && n_items <= chunk_hg_max_items()) {
+    if (KIND == Q4KV_Q8 && hd == 256u && gqa > 8u && gqa <= 16u && !IS_BATCH(MODE) &&
+        n_items <= chunk_hg_max_items()) {
         /* a few decode items with 9-16 query heads per KV head: the chunk
          * kernel in two head groups (grid.z) over the same rows; its shorter
          * per-workgroup chain beats the slab kernel where latency, not the
-         * doubled gather, bounds the launch */
+         * doubled gather, bounds the launch. Batch descriptors keep the slab
+         * kernel, which splits each item's own length: the chunk kernel's
+         * splits follow max_n, and a batch's max_n can far exceed most of
+         * its items (four list items under max_n 262144: 91 vs 12.8 us) */
         constexpr uint32_t CP = KCfg<KIND>::CP;
         /* 2 n_items workgroups per split, ceil(gqa / 2) heads' partials each */
         choose_split(2u * n_items, (max_n + CP - 1u) / CP, (gqa + 1u) / 2u, have_part, cap,

@@ -3,10 +3,15 @@ cache run the chunk kernel in two groups of query heads (grid.z: heads 0-7,
 then the rest) over the same rows. Every entry point family against the fp64
 oracle (|err| <= 2e-3 and <= 1e-3|ref| where |ref| >= 1), at head counts
 whose second group is full, partial and a single head, for one and several
-tokens, gated and not; and the held append riding in that launch."""
+tokens, gated and not; and the held append riding in that launch. Batch
+descriptors at these head counts (which keep the slab kernel) are checked
+beside them."""
+import ctypes
+
 import numpy as np
 import pytest
 
+import q4kv
 from gpu_util import note, quantize_on_gpu
 from synth import WIDTH, assert_attn_close, heads, selection
 
@@ -99,4 +104,47 @@ def test_head_groups_with_held_append(rt, oracle):
                        tok_stride=N_KVH * WIDTH, kvh_stride=WIDTH, max_kv=CTX, scale=1.0 / 16)
     assert_attn_close(got, want, what="held append gqa 13")
     for p in (kc, vc, dk, dv, dq, di, do):
+        rt.free(p)
+
+
+@pytest.mark.parametrize("gqa", [9, 12, 16])
+def test_head_groups_batch_descriptors(rt, oracle, gqa):
+    """q4_hip_qsa_decode_batch of four sequences sharing the caches, two with
+    per-KV-head lists and two with dense prefixes, gated."""
+    n_head, n_seq = gqa * N_KVH, 4
+    note(f"head groups batch gqa={gqa}")
+    rng = np.random.default_rng(8300 + gqa)
+    _, _, kc, vc, kb, vb = _setup(rt, oracle, rng)
+    q = heads(rng, (n_seq, n_head))
+    gate = rng.standard_normal((n_seq, n_head, HD)).astype(np.float32)
+    descs = (q4kv.SeqDesc * n_seq)()
+    owned, outs, want = [], [], []
+    for t in range(n_seq):
+        dq1, dg1 = rt.upload(q[t:t + 1]), rt.upload(gate[t:t + 1])
+        do1 = rt.alloc(q[t].nbytes)
+        owned += [dq1, dg1, do1]
+        if t % 2:
+            n_sel = CTX - 97 * t
+            descs[t] = q4kv.SeqDesc(kc, vc, dq1, dg1, do1, None, n_sel, 0, CTX, 0)
+            want.append(oracle.attn(q[t:t + 1], kb, vb, 2, n_head, N_KVH, HD, 1,
+                                    gate=gate[t:t + 1], kv_base=n_sel - 1, max_kv=CTX,
+                                    scale=1.0 / 16)[0])
+        else:
+            sel = np.stack([selection(rng, CTX - 1 - t) for _ in range(N_KVH)]).astype(np.int32)
+            di1 = rt.upload(sel)
+            owned.append(di1)
+            descs[t] = q4kv.SeqDesc(kc, vc, dq1, dg1, do1, di1, WIDTH, WIDTH, CTX, 0)
+            want.append(oracle.attn(q[t:t + 1], kb, vb, 2, n_head, N_KVH, HD, 1,
+                                    gate=gate[t:t + 1], idx=sel.ravel(), width=WIDTH,
+                                    tok_stride=N_KVH * WIDTH, kvh_stride=WIDTH, max_kv=CTX,
+                                    scale=1.0 / 16)[0])
+        outs.append(do1)
+    dd = rt.alloc(ctypes.sizeof(descs))
+    owned.append(dd)
+    assert rt.lib.q4_hip_h2d(dd, ctypes.addressof(descs), ctypes.sizeof(descs))
+    assert rt.lib.q4_hip_qsa_decode_batch(dd, n_seq, n_head, N_KVH, HD, 1.0 / 16, 2, CTX)
+    rt.sync()
+    got = np.stack([rt.download(o, q[0].nbytes, np.float32).reshape(n_head, HD) for o in outs])
+    assert_attn_close(got, np.stack(want), what=f"batch gqa {gqa}")
+    for p in owned + [kc, vc]:
         rt.free(p)
