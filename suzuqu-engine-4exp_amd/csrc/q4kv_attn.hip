@@ -1495,16 +1495,16 @@ __device__ static inline float ld_h(const uint8_t *p) {
 
 /* APP: the launch also performs a held append of one token's K/V rows at
  * the device position (as the step modes do with a descriptor's rows). */
-/* PIPE (prefill: one head group, many passes per wave): the K and V rows of
- * pass p + 1 are DMA'd while pass p is computed, K behind the P.V products,
- * V behind the next scores; the waits count the wave's own DMAs (issued from
- * inline assembly so that the compiler adds no wait of its own before the
- * LDS reads). */
+/* PIPE (one head group, two or more passes per wave: prefill, batched
+ * decode): the K and V rows of pass p + 1 are DMA'd while pass p is
+ * computed, K behind the P.V products, V behind the next scores; the waits
+ * count the wave's own DMAs (issued from inline assembly so that the compiler
+ * adds no wait of its own before the LDS reads). */
 template <int MODE, int HG, bool APP = false, bool PIPE = false>
 __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     constexpr bool STEPL = IS_STEP(MODE) || APP; /* a token's rows are appended */
-    static_assert(!PIPE || (HG == 1 && !STEPL && MODE == MODE_INDEXED),
-                  "the pipelined passes are the prefill instance's");
+    static_assert(!PIPE || (HG == 1 && !APP && MODE != MODE_PSTEP && MODE != MODE_DENSE),
+                  "the pipelined passes take one head group and a list or descriptors");
     constexpr uint32_t ROWB = 272, NCH = 17;
     constexpr uint32_t NSLAB = 4u / HG, NE = NSLAB * SLAB; /* slabs, entries per pass */
     constexpr uint32_t RBYTES = 2u * NE * ROWB;           /* K rows | V rows */
@@ -1562,6 +1562,16 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         const uint32_t e = j0 + slab * SLAB + (lane & 31u);
         if (e < j1) raw = it.list ? ldg(it.list + e) : (int32_t)e;
     }
+    /* PIPE: the list word of entry e (entry j0 past the split), one load for
+     * every lane; a batch item without a list reads a harmless word, and its
+     * position (the entry itself) is taken where the word is used */
+    auto list_word = [&](uint32_t e) -> int32_t {
+        const uint32_t jj = e < j1 ? e : j0;
+        if constexpr (IS_BATCH(MODE))
+            return ldg(it.lsrc + (jj & it.lmask));
+        else
+            return ldg(it.list + jj);
+    };
     /* MODE_STEP: every lane holds four fp32 of the token's K row and four of
      * its V row (lane l: block l >> 3, part l & 7); split 0's wave 0 writes
      * the quantised rows to the caches, and a wave whose slab lists the
@@ -1614,7 +1624,12 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
     auto issue = [&](uint32_t pass, uint32_t &ne, int32_t &pos) -> bool {
         const uint32_t e0 = j0 + pass * NE + slab * SLAB;
         ne = e0 < j1 ? min(SLAB, j1 - e0) : 0u;
-        pos = (raw >= 0 && (uint32_t)raw < it.max_kv && (lane & 31u) < ne) ? raw : -1;
+        int32_t rp = raw;
+        if constexpr (PIPE && IS_BATCH(MODE)) {
+            const uint32_t ee = e0 + (lane & 31u);
+            rp = (int32_t)(((uint32_t)raw & it.lmask) | ((ee < j1 ? ee : j0) & ~it.lmask));
+        }
+        pos = (rp >= 0 && (uint32_t)rp < it.max_kv && (lane & 31u) < ne) ? rp : -1;
         const bool any = __ballot(pos >= 0) != 0u;
         if (lane < 32u && hg == 0u) s_pos[slab * SLAB + lane] = pos;
         if (hg == 0u && any) {
@@ -1645,10 +1660,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
          * repeat of entry j0 past the split), so the DMA waits below count
          * exactly */
         if (n_pass > 0u && any) rows_dma(vbase, vrow, pos);
-        if (n_pass > 0u) {
-            const uint32_t e = j0 + NE + slab * SLAB + (lane & 31u);
-            raw = ldg(it.list + (e < j1 ? e : j0));
-        }
+        if (n_pass > 0u) raw = list_word(j0 + NE + slab * SLAB + (lane & 31u));
     }
     TRACEW(1);
 
@@ -1840,6 +1852,15 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             cur = nxt;
         }
     };
+    /* the appended token's quantised row (x: this lane's four values of
+     * block lane >> 3) stored into the slab rows of mask hit */
+    auto subst_rows = [&](uint64_t hit, uint8_t *rows_base, const float (&x)[4]) {
+        int q[4];
+        const float d = q8_lane_quant(x[0], x[1], x[2], x[3], q);
+        for (uint64_t m = hit; m; m &= m - 1u)
+            q8_lane_store(rows_base + (uint32_t)__builtin_ctzll(m) * ROWB + 34u * (lane >> 3),
+                          lane & 7u, d, q);
+    };
     /* padding rows (never fetched, or fetched from row 0): zero their K block
      * scales */
     auto k_fix = [&]() {
@@ -1863,9 +1884,15 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
         for (uint32_t pass = 0; pass < n_pass; pass++) {
             /* pass p's K rows have landed when at most its V rows (9 DMA
              * instructions) and the next list load are outstanding */
+            /* rows at the appended position take the new token's bytes: K
+             * once K has landed, V once V has */
+            const uint64_t hit =
+                STEPL && any ? __ballot(lane < 32u && pos >= 0 && (uint32_t)pos == it.pos_new)
+                             : 0ull;
             if (any) {
                 __builtin_amdgcn_s_waitcnt(0x0F7A); /* vmcnt(10) */
                 TRACEW(3);
+                if (STEPL && hit) subst_rows(hit, krow, nk);
                 k_fix();
                 scores_softmax(pass);
             }
@@ -1874,6 +1901,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
              * has no load of its own pending later (its wait would also
              * drain the next pass's DMA) */
             asm volatile("" ::"v"(raw));
+            if (STEPL && hit) subst_rows(hit, vrow, nv);
             if (any) v_fix();
             /* pass p + 1: its K rows behind this pass's P.V, its V rows behind
              * its own scores, then pass p + 2's list entries (one load always) */
@@ -1882,10 +1910,7 @@ __global__ __launch_bounds__(256, 2) void qsa_slab_k(AttnArgs a) {
             const bool any_n = pass + 1u < n_pass ? issue(pass + 1u, ne_n, pos_n) : false;
             if (any) pv();
             if (any_n) rows_dma(vbase, vrow, pos_n);
-            {
-                const uint32_t e = j0 + (pass + 2u) * NE + slab * SLAB + (lane & 31u);
-                raw = ldg(it.list + (e < j1 ? e : j0));
-            }
+            raw = list_word(j0 + (pass + 2u) * NE + slab * SLAB + (lane & 31u));
             any = any_n;
             pos = pos_n;
             ne = ne_n;
@@ -3697,9 +3722,11 @@ static bool launch_kind(AttnArgs a, uint32_t n_items, uint32_t max_n, uint32_t g
             }
         } else if (pl.slab && pl.hg == 1u) {
             bool piped = false;
-            if constexpr (MODE == MODE_INDEXED) {
-                /* prefill-sized splits: the pipelined passes */
-                if (S == 1u && a.idx && slab_pipe_enabled()) {
+            if constexpr (MODE == MODE_INDEXED || MODE == MODE_BATCH || MODE == MODE_STEP) {
+                /* two or more passes per wave (a split's entries over 128 per
+                 * pass): the pipelined passes */
+                const uint32_t per_split = (max_n + S - 1u) / S;
+                if (per_split > 128u && (MODE != MODE_INDEXED || a.idx) && slab_pipe_enabled()) {
                     qsa_slab_k<MODE, 1, false, true><<<grid, 256, 0, q4kv_stream>>>(a);
                     piped = true;
                 }
