@@ -39,6 +39,7 @@
 #include "q4kv.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <utility>
 
 namespace {
@@ -630,7 +631,37 @@ template <uint32_t KPT> struct TopkShape {
     static constexpr int WG_PER_CU = KPT <= 8u ? 2 : 1;
 };
 
-template <int SRC, uint32_t KPT>
+/* Split selection of one device-position row of up to 65536 keys: workgroup
+ * w of G reduces keys w*4096 .. +4095 to its local candidates (its keys
+ * within the distance bin where its own count reaches need: every key of
+ * the row's top need is among them, since such a key has fewer than need
+ * greater keys in the row, so in its slice), in index order, plus its
+ * distance histogram and maximum. The last workgroup to finish (a ticket
+ * taken after an agent-scope release) merges the G histograms, keeps the
+ * candidates at or above the row's bin and finishes as the one-workgroup
+ * kernel does. One buffer per GPU: launches on one GPU must not overlap
+ * (the library issues every launch on its one stream). */
+constexpr uint32_t TKS_G = 16;        /* most workgroups of a split row */
+constexpr uint32_t TKS_CAPW = 1024;   /* local candidates per workgroup */
+constexpr uint32_t TKS_HC = 8;        /* local histogram copies */
+struct TopkSplitScratch {
+    uint32_t hist[TKS_G][TK_DBINS];
+    uint32_t mx[TKS_G], cnt[TKS_G]; /* cnt 0xffffffff: more than TKS_CAPW */
+    uint32_t ticket;
+    uint32_t key[TKS_G][TKS_CAPW];
+    uint32_t idx[TKS_G][TKS_CAPW];
+};
+/* agent-scope (sc1) accesses of the split scratch */
+__device__ inline void st_agent(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline uint32_t ld_agent(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int TKS_SC1 = 16; /* buffer-load cache policy: sc1 */
+__device__ TopkSplitScratch tks_scratch;
+
+template <int SRC, uint32_t KPT, uint32_t SPLIT = 0>
 __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(const float *score, int32_t *sel,
                                                    uint32_t stride, uint32_t k_blk,
                                                    uint32_t ratio, uint32_t pos0,
@@ -638,24 +669,28 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                                                    const q4kv_index_desc *descs) {
     constexpr uint32_t HC = TopkShape<KPT>::HC, CAP = TopkShape<KPT>::CAP;
     __shared__ TopkSmem<HC, CAP> sm;
+    static_assert(!SPLIT || SRC == TK_DEV, "split rows are device-position rows");
+    /* t: the row (token or batch item); with SPLIT the slice of the one row */
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t rowi = SPLIT ? 0u : t;
     uint32_t pos;
     const float *row;
     int32_t *out;
     if (SRC == TK_BATCH) {
-        const q4kv_index_desc *d = descs + t;
+        const q4kv_index_desc *d = descs + rowi;
         pos = ldg(&d->pos);
         row = q4kv_gptr_at(&d->score);
         out = q4kv_gptr_at(&d->sel);
     } else {
-        pos = (SRC == TK_DEV ? (uint32_t)*pp : pos0) + t;
-        row = score + (size_t)t * stride;
-        out = sel + (size_t)t * width;
+        pos = (SRC == TK_DEV ? (uint32_t)*pp : pos0) + rowi;
+        row = score + (size_t)rowi * stride;
+        out = sel + (size_t)rowi * width;
     }
     const uint32_t n_vis = (pos + 1) / ratio;
     const uint32_t need = n_vis < k_blk ? n_vis : k_blk;
     if (need == n_vis) { /* every complete block fits: the dense prefix */
+        if (SPLIT && t != 0) return;
         for (uint32_t w = tid; w < width; w += TK_T) stg(out + w, w <= pos ? (int32_t)w : -1);
         return;
     }
@@ -697,7 +732,235 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
     auto valid = [&](uint32_t c, uint32_t r) { return c * TK_CHUNK + r * TK_T + tid < n_vis; };
 
     bool fast = nchunk == 1;
-    if (fast) {
+    uint32_t above = 0, ncand = 0, Kc = 0;
+    if constexpr (SPLIT != 0) {
+        /* ---- this workgroup's slice (SK keys, SPLIT per thread): keys,
+         * maximum, distance histogram ---- */
+        constexpr uint32_t KS = SPLIT, SK = TK_T * KS;
+        constexpr uint32_t GMAX = TK_CHUNK / SK, P = TKS_G / GMAX; /* waves per slice */
+        constexpr uint32_t LR = TKS_CAPW / P, LK = LR / 64u; /* list entries per wave, per lane */
+        const uint32_t G = gridDim.x, base = t * SK;
+        const uint32_t lim = n_vis > base ? min(n_vis - base, SK) : 0u;
+        TopkSplitScratch &gs = tks_scratch;
+        for (uint32_t i = tid; i < TK_DBINS * TKS_HC; i += TK_T) sm.h.dist[i] = 0;
+        uint32_t ks[KS];
+        {
+            /* loads past the slice's visible keys return 0 (buffer bound),
+             * whose key is then 0, as load_chunk's partial chunk */
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(row + base), (short)0, (int)(lim * 4u), 0x00020000);
+#pragma unroll
+            for (uint32_t r = 0; r < KS; r++)
+                ks[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(tid * 4u),
+                                                             (int)(r * TK_T * 4u), 0);
+#pragma unroll
+            for (uint32_t r = 0; r < KS; r++) {
+                const uint32_t u = ks[r];
+                const uint32_t in = (r * TK_T + tid - lim) & 0x80000000u;
+                ks[r] = u ^ ((uint32_t)((int32_t)u >> 31) | in);
+            }
+        }
+        uint32_t mx = 0;
+#pragma unroll
+        for (uint32_t r = 0; r < KS; r++) mx = max(mx, ks[r]);
+        mx = wave_max_u32(mx);
+        if (lane == 0) sm.wtot[1][wave] = mx;
+        __syncthreads();
+        uint32_t M = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < 16; w++) M = max(M, sm.wtot[1][w]);
+        const uint32_t Mb = M >> TK_DSHIFT;
+        uint32_t dist[KS];
+#pragma unroll
+        for (uint32_t r = 0; r < KS; r++) {
+            dist[r] = min(Mb - (ks[r] >> TK_DSHIFT), TK_DBINS - 1u);
+            if (r * TK_T + tid < lim)
+                atomicAdd(sm.h.dist + (lane & (TKS_HC - 1u)) + dist[r] * TKS_HC, 1u);
+        }
+        __syncthreads();
+        if (tid < TK_DBINS) { /* fold the copies, in an order rotated by the bin */
+            const uint32_t *hp = sm.h.dist + tid * TKS_HC;
+            uint32_t v = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < TKS_HC; i++) v += hp[(i + tid) & (TKS_HC - 1u)];
+            sm.bins[tid] = v;
+            st_agent(&gs.hist[t][tid], v);
+        }
+        if (tid == 0) sm.st[0] = TK_DBINS - 1u; /* fewer than need keys: all */
+        __syncthreads();
+        if (wave == 0) { /* the nearest bin where this slice's count reaches need */
+            uint32_t c[8], s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) { c[i] = sm.bins[8u * lane + i]; s += c[i]; }
+            uint32_t acc = wave_incl_scan(s) - s;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (acc < need && acc + c[i] >= need) sm.st[0] = 8u * lane + i;
+                acc += c[i];
+            }
+        }
+        __syncthreads();
+        /* ---- local candidates in index order: (r, wave) counts by ballot,
+         * one wave scan over the 16 KS groups (KS / 4 per lane) ---- */
+        const uint32_t Bw = sm.st[0];
+        uint64_t cm[KS];
+#pragma unroll
+        for (uint32_t r = 0; r < KS; r++) {
+            cm[r] = __ballot((r * TK_T + tid < lim) & (dist[r] <= Bw));
+            if (lane == 0) sm.cg[r * 16u + wave] = (uint32_t)__popcll(cm[r]);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            constexpr uint32_t GL = KS / 4u; /* groups per lane */
+            uint32_t v[GL], s = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < GL; i++) { v[i] = sm.cg[GL * lane + i]; s += v[i]; }
+            const uint32_t inc = wave_incl_scan(s);
+            uint32_t o = inc - s;
+#pragma unroll
+            for (uint32_t i = 0; i < GL; i++) { sm.ce[GL * lane + i] = o; o += v[i]; }
+            if (lane == 63) sm.st[1] = inc;
+        }
+        __syncthreads();
+        const uint32_t cw = sm.st[1];
+        if (cw <= TKS_CAPW) {
+#pragma unroll
+            for (uint32_t r = 0; r < KS; r++) {
+                if ((cm[r] >> lane) & 1u) {
+                    const uint32_t i = sm.ce[r * 16u + wave] + lanes_below(cm[r]);
+                    st_agent(&gs.key[t][i], ks[r]);
+                    st_agent(&gs.idx[t][i], base + r * TK_T + tid);
+                }
+            }
+        }
+        if (tid == 0) {
+            st_agent(&gs.mx[t], M);
+            st_agent(&gs.cnt[t], cw <= TKS_CAPW ? cw : 0xffffffffu);
+        }
+        /* ---- the ticket. Everything the merge reads is stored and loaded
+         * at agent scope (sc1: coherent across the XCDs' L2s), so the last
+         * workgroup needs no L2 invalidate (an acquire fence costs ~1.5 us
+         * here): each wave waits for its stores, and after the barrier one
+         * release orders them before the ticket ---- */
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            sm.st[3] = __hip_atomic_fetch_add(&gs.ticket, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (sm.st[3] != G - 1u) return;
+        if (tid == 0) st_agent(&gs.ticket, 0u);
+        /* ---- one round trip for everything the merge reads: the slices'
+         * maxima and counts, their histograms (thread: bin hb of slices
+         * hw0, hw0 + 2, ...) and their lists (wave w: part w % P of slice
+         * w / P, LK entries per lane; entries past a list's count are
+         * masked after) ---- */
+        uint32_t mxv = 0, cntv = 0;
+        if (tid < G) {
+            mxv = ld_agent(&gs.mx[tid]);
+            cntv = ld_agent(&gs.cnt[tid]);
+        }
+        const uint32_t hb = tid & (TK_DBINS - 1u), hw0 = tid / TK_DBINS;
+        constexpr uint32_t HL = (GMAX + 1u) / 2u;
+        uint32_t hv[HL];
+#pragma unroll
+        for (uint32_t i = 0; i < HL; i++)
+            hv[i] = ld_agent(&gs.hist[min(hw0 + 2u * i, G - 1u)][hb]);
+        const uint32_t ls = min(wave / P, G - 1u), lp = wave % P;
+        uint32_t kk[LK], ii[LK];
+        {
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)&gs.key[ls][lp * LR], (short)0, (int)(LR * 4u), 0x00020000);
+            const __amdgpu_buffer_rsrc_t ri = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)&gs.idx[ls][lp * LR], (short)0, (int)(LR * 4u), 0x00020000);
+#pragma unroll
+            for (uint32_t i = 0; i < LK; i++)
+                kk[i] = __builtin_amdgcn_raw_buffer_load_b32(rk, (int)(lane * 4u), (int)(i * 256u),
+                                                             TKS_SC1);
+#pragma unroll
+            for (uint32_t i = 0; i < LK; i++)
+                ii[i] = __builtin_amdgcn_raw_buffer_load_b32(ri, (int)(lane * 4u), (int)(i * 256u),
+                                                             TKS_SC1);
+        }
+        if (tid < G) {
+            sm.cg[tid] = mxv;
+            sm.ce[tid] = cntv;
+        }
+        if (tid < TK_DBINS) sm.bins[tid] = 0;
+        for (uint32_t i = tid; i < (1u << TK_CBITS); i += TK_T) sm.h.cand[i] = 0;
+        if (tid == 0) sm.st[0] = TK_DBINS - 1u;
+        __syncthreads();
+        uint32_t Mg = 0;
+        bool ovf = false;
+        for (uint32_t w = 0; w < G; w++) {
+            Mg = max(Mg, sm.cg[w]);
+            ovf |= sm.ce[w] == 0xffffffffu;
+        }
+        const uint32_t Mgb = Mg >> TK_DSHIFT;
+#pragma unroll
+        for (uint32_t i = 0; i < HL; i++) {
+            const uint32_t w = hw0 + 2u * i;
+            if (w < G && hv[i])
+                atomicAdd(&sm.bins[min(hb + (Mgb - (sm.cg[w] >> TK_DSHIFT)), TK_DBINS - 1u)], hv[i]);
+        }
+        __syncthreads();
+        if (wave == 0) { /* the nearest bin where the row's count reaches need */
+            uint32_t c[8], s = 0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) { c[i] = sm.bins[8u * lane + i]; s += c[i]; }
+            uint32_t acc = wave_incl_scan(s) - s;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (acc < need && acc + c[i] >= need) {
+                    sm.st[0] = 8u * lane + i;
+                    sm.st[1] = acc;
+                }
+                acc += c[i];
+            }
+        }
+        __syncthreads();
+        const uint32_t B = sm.st[0];
+        above = sm.st[1];
+        Kc = (Mgb - B) << TK_DSHIFT;
+        fast = B < min(Mgb, TK_DBINS - 1u) && !ovf && n_vis <= G * SK;
+        if (fast) {
+            /* ---- the lists' keys >= Kc; the waves' survivor counts in wave
+             * order (slice, then part: index order) give each its offset ---- */
+            const uint32_t cnt_w = wave / P < G ? sm.ce[wave / P] : 0u;
+            const uint32_t e0 = lp * LR + lane;
+            uint32_t n = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < LK; i++)
+                n += (uint32_t)__popcll(__ballot(kk[i] >= Kc && e0 + 64u * i < cnt_w));
+            if (lane == 0) sm.wtot[2][wave] = n;
+            __syncthreads();
+            uint32_t o = 0, tot = 0;
+#pragma unroll
+            for (uint32_t w = 0; w < 16u; w++) {
+                const uint32_t v = sm.wtot[2][w];
+                o += w < wave ? v : 0u;
+                tot += v;
+            }
+            fast = tot <= CAP;
+            ncand = tot;
+            if (fast) {
+#pragma unroll
+                for (uint32_t i = 0; i < LK; i++) {
+                    const bool keep = kk[i] >= Kc && e0 + 64u * i < cnt_w;
+                    const uint64_t m = __ballot(keep);
+                    if (keep) {
+                        const uint32_t p = o + lanes_below(m);
+                        sm.ckey[p] = kk[i];
+                        sm.cidx[p] = (int32_t)ii[i];
+                    }
+                    o += (uint32_t)__popcll(m);
+                }
+            }
+            __syncthreads();
+        }
+    } else if (fast) {
         for (uint32_t i = tid; i < TK_DBINS * HC; i += TK_T) sm.h.dist[i] = 0;
         sm.wm[tid] = 0;
         load_chunk(0);
@@ -747,10 +1010,12 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
             }
         }
         __syncthreads();
-        const uint32_t B = sm.st[0], above = sm.st[1], ncand = sm.st[2];
+        const uint32_t B = sm.st[0];
+        above = sm.st[1];
+        ncand = sm.st[2];
         /* the clamped last bin and the padding keys' bin take the full path */
         fast = B < min(Mb, TK_DBINS - 1u) && ncand <= CAP;
-        const uint32_t Kc = (Mb - B) << TK_DSHIFT; /* candidates: key >= Kc */
+        Kc = (Mb - B) << TK_DSHIFT; /* candidates: key >= Kc */
         if (fast) {
             /* ---- ordered compaction of the candidates: each lane's 64-bit
              * row mask, the (row, wave) lane masks by LDS atomic-or, one
@@ -780,69 +1045,72 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                 sm.cidx[i] = (int32_t)e;
             }
             __syncthreads();
-            /* ---- exact threshold inside bin B: its keys share the bits above
-             * bit 19; two radix passes (10 + 9 bits) over those candidates ---- */
-            const uint32_t kb = Kc >> TK_DSHIFT;
-            uint32_t pre = 0, gt = above;
-            for (uint32_t pass = 0; pass < 2; pass++) {
-                const uint32_t lo = pass == 0 ? 9u : 0u, wbits = pass == 0 ? 10u : 9u;
-                const uint32_t nd = 1u << wbits;
-                for (uint32_t i = tid; i < ncand; i += TK_T) {
-                    const uint32_t u = sm.ckey[i];
-                    const uint32_t v = u & ((1u << TK_DSHIFT) - 1u);
-                    if ((u >> TK_DSHIFT) == kb && (pass == 0 || (v >> 9) == pre))
-                        atomicAdd(&sm.h.cand[(v >> lo) & (nd - 1u)], 1u);
-                }
-                __syncthreads();
-                /* thread t owns digit nd-1-t (descending) */
-                const int d = (int)nd - 1 - (int)tid;
-                const uint32_t c = d >= 0 ? sm.h.cand[d] : 0u;
-                const uint32_t acc = block_excl_scan_nb(c, sm.wtot[pass]);
-                const uint32_t target = need - gt;
-                if (acc < target && acc + c >= target) {
-                    sm.st[4 + 2 * pass] = (uint32_t)d;
-                    sm.st[5 + 2 * pass] = acc;
-                }
-                __syncthreads();
-                if (d >= 0) sm.h.cand[d] = 0;
-                pre = pass == 0 ? sm.st[4] : (pre << 9) | sm.st[6];
-                gt += sm.st[5 + 2 * pass];
-                __syncthreads();
-            }
-            const uint32_t thr = Kc | pre;
-            const uint32_t n_gt = gt, rem = need - n_gt;
-            /* ---- ordered output over the index-ordered candidates ---- */
-            uint32_t g = 0, e = 0;
-            const uint32_t i0 = 4u * tid;
-#pragma unroll
-            for (uint32_t j = 0; j < 4; j++) {
-                const uint32_t i = i0 + j;
-                if (i < ncand) {
-                    g += sm.ckey[i] > thr;
-                    e += sm.ckey[i] == thr;
-                }
-            }
-            const uint32_t pk = block_excl_scan_nb(g | (e << 16), sm.wtot[2]);
-            uint32_t og = pk & 0xffffu, oe = pk >> 16;
-#pragma unroll
-            for (uint32_t j = 0; j < 4; j++) {
-                const uint32_t i = i0 + j;
-                if (i < ncand) {
-                    const uint32_t u = sm.ckey[i];
-                    if (u > thr) {
-                        if (og < TK_MAXK) sm.chosen[og] = sm.cidx[i];
-                        og++;
-                    } else if (u == thr) {
-                        if (oe < rem && n_gt + oe < TK_MAXK) sm.chosen[n_gt + oe] = sm.cidx[i];
-                        oe++;
-                    }
-                }
+        }
+    }
+    if (fast) {
+        /* ---- exact threshold inside bin B: its keys share the bits above
+         * bit 19; two radix passes (10 + 9 bits) over those candidates ---- */
+        const uint32_t kb = Kc >> TK_DSHIFT;
+        uint32_t pre = 0, gt = above;
+        for (uint32_t pass = 0; pass < 2; pass++) {
+            const uint32_t lo = pass == 0 ? 9u : 0u, wbits = pass == 0 ? 10u : 9u;
+            const uint32_t nd = 1u << wbits;
+            for (uint32_t i = tid; i < ncand; i += TK_T) {
+                const uint32_t u = sm.ckey[i];
+                const uint32_t v = u & ((1u << TK_DSHIFT) - 1u);
+                if ((u >> TK_DSHIFT) == kb && (pass == 0 || (v >> 9) == pre))
+                    atomicAdd(&sm.h.cand[(v >> lo) & (nd - 1u)], 1u);
             }
             __syncthreads();
+            /* thread t owns digit nd-1-t (descending) */
+            const int d = (int)nd - 1 - (int)tid;
+            const uint32_t c = d >= 0 ? sm.h.cand[d] : 0u;
+            const uint32_t acc = block_excl_scan_nb(c, sm.wtot[pass]);
+            const uint32_t target = need - gt;
+            if (acc < target && acc + c >= target) {
+                sm.st[4 + 2 * pass] = (uint32_t)d;
+                sm.st[5 + 2 * pass] = acc;
+            }
+            __syncthreads();
+            if (d >= 0) sm.h.cand[d] = 0;
+            pre = pass == 0 ? sm.st[4] : (pre << 9) | sm.st[6];
+            gt += sm.st[5 + 2 * pass];
+            __syncthreads();
         }
+        const uint32_t thr = Kc | pre;
+        const uint32_t n_gt = gt, rem = need - n_gt;
+        /* ---- ordered output over the index-ordered candidates ---- */
+        uint32_t g = 0, e = 0;
+        const uint32_t i0 = 4u * tid;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            const uint32_t i = i0 + j;
+            if (i < ncand) {
+                g += sm.ckey[i] > thr;
+                e += sm.ckey[i] == thr;
+            }
+        }
+        const uint32_t pk = block_excl_scan_nb(g | (e << 16), sm.wtot[2]);
+        uint32_t og = pk & 0xffffu, oe = pk >> 16;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            const uint32_t i = i0 + j;
+            if (i < ncand) {
+                const uint32_t u = sm.ckey[i];
+                if (u > thr) {
+                    if (og < TK_MAXK) sm.chosen[og] = sm.cidx[i];
+                    og++;
+                } else if (u == thr) {
+                    if (oe < rem && n_gt + oe < TK_MAXK) sm.chosen[n_gt + oe] = sm.cidx[i];
+                    oe++;
+                }
+            }
+        }
+        __syncthreads();
     }
     if (!fast) {
         /* ---- full path: four 8-bit radix passes over every key ---- */
+        if (SPLIT && nchunk == 1) load_chunk(0);
         if (tid == 0) { sm.st[4] = 0; sm.st[5] = 0; }
         for (uint32_t pass = 0; pass < 4; pass++) {
             for (uint32_t i = tid; i < 256 * HC; i += TK_T) sm.h.rep[i] = 0;
@@ -1180,6 +1448,19 @@ extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok
             score, sel, stride, k_blk, ratio, pos0, width, nullptr, nullptr);
     return q4kv_launch_ok("qsa_topk");
 }
+/* Keys per thread of a split device-position row's slices (4, 8 or 16:
+ * 16, 8 or 4 workgroups for 65536 keys); Q4KV_TOPK_SPLIT=0 keeps the row on
+ * one workgroup. */
+static uint32_t topk_split_kps(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_TOPK_SPLIT");
+        const int x = e ? atoi(e) : 8;
+        v = (x == 0 || x == 4 || x == 8 || x == 16) ? x : 8;
+    }
+    return (uint32_t)v;
+}
+
 extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride,
                                   uint32_t k_blk, uint32_t ratio, uint32_t width) {
     Q4KV_FLUSH_OR_FAIL();
@@ -1188,13 +1469,27 @@ extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t str
         return false;
     (void)hipGetLastError();
     /* the device position is unknown here: the row capacity (stride blocks)
-     * decides the register layout; 0 means unknown */
-    if (stride && stride <= 16u * TK_T)
-        qsa_topk_k<TK_DEV, 16><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0,
-                                                             width, q4kv_pos_d, nullptr);
+     * decides the register layout; 0 means unknown. Rows of 16385-65536
+     * blocks are split over slices of 1024 x kps blocks. */
+    const uint32_t kps = stride > 16u * TK_T && stride <= TK_T * TK_KPT ? topk_split_kps() : 0u;
+    if (kps) {
+        const uint32_t g = (stride + TK_T * kps - 1u) / (TK_T * kps);
+        if (kps == 4)
+            qsa_topk_k<TK_DEV, TK_KPT, 4><<<g, TK_T, 0, q4kv_stream>>>(
+                score, sel, stride, k_blk, ratio, 0, width, q4kv_pos_d, nullptr);
+        else if (kps == 8)
+            qsa_topk_k<TK_DEV, TK_KPT, 8><<<g, TK_T, 0, q4kv_stream>>>(
+                score, sel, stride, k_blk, ratio, 0, width, q4kv_pos_d, nullptr);
+        else
+            qsa_topk_k<TK_DEV, TK_KPT, 16><<<g, TK_T, 0, q4kv_stream>>>(
+                score, sel, stride, k_blk, ratio, 0, width, q4kv_pos_d, nullptr);
+    } else if (stride && stride <= 16u * TK_T)
+        qsa_topk_k<TK_DEV, 16><<<1, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk, ratio,
+                                                             0, width, q4kv_pos_d, nullptr);
     else
-        qsa_topk_k<TK_DEV, TK_KPT><<<1, TK_T, 0, q4kv_stream>>>(score, sel, 0, k_blk, ratio, 0,
-                                                                 width, q4kv_pos_d, nullptr);
+        qsa_topk_k<TK_DEV, TK_KPT><<<1, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk,
+                                                                 ratio, 0, width, q4kv_pos_d,
+                                                                 nullptr);
     return q4kv_launch_ok("qsa_topk_d");
 }
 

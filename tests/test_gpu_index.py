@@ -36,6 +36,8 @@ def _score_rows(rng, n_vis):
     z[rng.integers(0, n_vis, 40)] = 1.0
     yield "signed-zeros", z
     yield "all-equal", np.full(n_vis, 2.5, np.float32)
+    # rising with the index: the whole selection in the last slices of a split row
+    yield "ascending", np.linspace(0.0, 1.0, n_vis, dtype=np.float32)
     n = rng.standard_normal(n_vis).astype(np.float32)
     n[rng.integers(0, n_vis, 7)] = np.nan
     n[rng.integers(0, n_vis, 5)] = -np.inf
@@ -43,14 +45,20 @@ def _score_rows(rng, n_vis):
 
 
 # ----------------------------------------------------------------- top-k
-@pytest.mark.parametrize("pos", [0, 2, 3, 2047, 2048, 2051, 5000, 65539, 262143, 300001])
-def test_topk_d_bit_exact(rt, oracle, pos):
+@pytest.mark.parametrize("cap", ["tight", "wide"])
+@pytest.mark.parametrize("pos", [0, 2, 3, 2047, 2048, 2051, 5000, 65539, 262139, 262143, 300001])
+def test_topk_d_bit_exact(rt, oracle, pos, cap):
+    """Row capacity (stride) just past the visible blocks, or a whole number
+    of 65536-key chunks beyond them, which the kernel then loads unmasked;
+    either way the 9.0 filler past n_vis must never be selected."""
     lib = rt.lib
     rng = np.random.default_rng(100 + pos)
     n_vis = (pos + 1) // RATIO
     stride = max(n_vis, 1) + 5
+    if cap == "wide":
+        stride = -(-stride // 65536) * 65536
     for name, row in _score_rows(rng, max(n_vis, 1)):
-        note(f"topk_d pos={pos} rows={name}")
+        note(f"topk_d pos={pos} cap={cap} rows={name}")
         sc = np.full((1, stride), 9.0, np.float32)   # past n_vis: never read as a score
         sc[0, :row.size] = row
         d_sc, d_sel = rt.upload(sc), rt.alloc(WIDTH * 4)
@@ -70,6 +78,7 @@ def test_topk_rows_bit_exact(rt, oracle):
     lib = rt.lib
     for pos0, n_tok, k_blk, width, stride in [(2040, 20, K_BLK, WIDTH, 600),
                                               (9000, 33, 100, 300, 2300),
+                                              (9000, 33, 100, 300, 8192),
                                               (70000, 6, K_BLK, WIDTH, 17503)]:
         note(f"topk rows pos0={pos0} n_tok={n_tok} k_blk={k_blk}")
         rng = np.random.default_rng(pos0)
