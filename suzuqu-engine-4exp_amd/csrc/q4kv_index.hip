@@ -641,7 +641,8 @@ template <uint32_t KPT> struct TopkShape {
  * candidates at or above the row's bin and finishes as the one-workgroup
  * kernel does. One buffer per GPU: launches on one GPU must not overlap
  * (the library issues every launch on its one stream). */
-constexpr uint32_t TKS_G = 16;        /* most workgroups of a split row */
+constexpr uint32_t TKS_KPS = 8;       /* keys per thread of a slice: 8192-key slices */
+constexpr uint32_t TKS_G = 8;         /* most slices of a row (65536 keys) */
 constexpr uint32_t TKS_CAPW = 1024;   /* local candidates per workgroup */
 constexpr uint32_t TKS_HC = 8;        /* local histogram copies */
 struct TopkSplitScratch {
@@ -737,7 +738,8 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         /* ---- this workgroup's slice (SK keys, SPLIT per thread): keys,
          * maximum, distance histogram ---- */
         constexpr uint32_t KS = SPLIT, SK = TK_T * KS;
-        constexpr uint32_t GMAX = TK_CHUNK / SK, P = TKS_G / GMAX; /* waves per slice */
+        constexpr uint32_t GMAX = TK_CHUNK / SK, P = (TK_T / 64u) / GMAX; /* waves per slice */
+        static_assert(GMAX <= TKS_G && P >= 1u, "slices fit the scratch and the waves");
         constexpr uint32_t LR = TKS_CAPW / P, LK = LR / 64u; /* list entries per wave, per lane */
         const uint32_t G = gridDim.x, base = t * SK;
         const uint32_t lim = n_vis > base ? min(n_vis - base, SK) : 0u;
@@ -1448,17 +1450,14 @@ extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok
             score, sel, stride, k_blk, ratio, pos0, width, nullptr, nullptr);
     return q4kv_launch_ok("qsa_topk");
 }
-/* Keys per thread of a split device-position row's slices (4, 8 or 16:
- * 16, 8 or 4 workgroups for 65536 keys); Q4KV_TOPK_SPLIT=0 keeps the row on
- * one workgroup. */
-static uint32_t topk_split_kps(void) {
+/* Q4KV_TOPK_SPLIT=0 keeps a device-position row on one workgroup. */
+static bool topk_split_enabled(void) {
     static int v = -1;
     if (v < 0) {
         const char *e = getenv("Q4KV_TOPK_SPLIT");
-        const int x = e ? atoi(e) : 8;
-        v = (x == 0 || x == 4 || x == 8 || x == 16) ? x : 8;
+        v = (e && e[0] == '0') ? 0 : 1;
     }
-    return (uint32_t)v;
+    return v != 0;
 }
 
 extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t stride,
@@ -1470,19 +1469,11 @@ extern "C" bool q4_hip_qsa_topk_d(const float *score, int32_t *sel, uint32_t str
     (void)hipGetLastError();
     /* the device position is unknown here: the row capacity (stride blocks)
      * decides the register layout; 0 means unknown. Rows of 16385-65536
-     * blocks are split over slices of 1024 x kps blocks. */
-    const uint32_t kps = stride > 16u * TK_T && stride <= TK_T * TK_KPT ? topk_split_kps() : 0u;
-    if (kps) {
-        const uint32_t g = (stride + TK_T * kps - 1u) / (TK_T * kps);
-        if (kps == 4)
-            qsa_topk_k<TK_DEV, TK_KPT, 4><<<g, TK_T, 0, q4kv_stream>>>(
-                score, sel, stride, k_blk, ratio, 0, width, q4kv_pos_d, nullptr);
-        else if (kps == 8)
-            qsa_topk_k<TK_DEV, TK_KPT, 8><<<g, TK_T, 0, q4kv_stream>>>(
-                score, sel, stride, k_blk, ratio, 0, width, q4kv_pos_d, nullptr);
-        else
-            qsa_topk_k<TK_DEV, TK_KPT, 16><<<g, TK_T, 0, q4kv_stream>>>(
-                score, sel, stride, k_blk, ratio, 0, width, q4kv_pos_d, nullptr);
+     * blocks are split over slices of TK_T * TKS_KPS blocks. */
+    if (stride > 16u * TK_T && stride <= TK_T * TK_KPT && topk_split_enabled()) {
+        const uint32_t g = (stride + TK_T * TKS_KPS - 1u) / (TK_T * TKS_KPS);
+        qsa_topk_k<TK_DEV, TK_KPT, TKS_KPS><<<g, TK_T, 0, q4kv_stream>>>(
+            score, sel, stride, k_blk, ratio, 0, width, q4kv_pos_d, nullptr);
     } else if (stride && stride <= 16u * TK_T)
         qsa_topk_k<TK_DEV, 16><<<1, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk, ratio,
                                                              0, width, q4kv_pos_d, nullptr);
