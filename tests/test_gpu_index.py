@@ -72,6 +72,47 @@ def test_topk_d_bit_exact(rt, oracle, pos, cap):
         assert np.array_equal(got, want), (pos, name, np.flatnonzero(got != want)[:8])
 
 
+def test_topk_d_split_row_graph_replays(rt, oracle):
+    """Rows of 16385-65536 blocks are selected by 8 slice workgroups that hand
+    their candidates to the last one through a per-GPU buffer and ticket. A
+    captured topk_d replayed at positions filling 3, 8 and 5 slices and a
+    dense prefix, with an eager call on another row between replays: every
+    list bit-exact against the oracle (the ticket is re-armed by each launch,
+    the buffer reused)."""
+    lib = rt.lib
+    rng = np.random.default_rng(4242)
+    stride = 65536
+    row = np.maximum(rng.standard_normal(stride) * 6, 0).astype(np.float32)
+    other = rng.standard_normal(stride).astype(np.float32)
+    d_sc, d_sel = rt.upload(row[None, :]), rt.alloc(WIDTH * 4)
+    d_o, d_osel = rt.upload(other[None, :]), rt.alloc(WIDTH * 4)
+    lib.q4_hip_pos_push(100000)
+    assert lib.q4_hip_graph_begin() == 1
+    ok = lib.q4_hip_qsa_topk_d(d_sc, d_sel, stride, K_BLK, RATIO, WIDTH)
+    g = lib.q4_hip_graph_end()
+    assert ok and g
+    try:
+        for pos in (80003, 262143, 170001, 1500, 262140):
+            note(f"split topk_d graph replay pos={pos}")
+            lib.q4_hip_pos_push(pos)
+            assert lib.q4_hip_graph_launch(g)
+            rt.sync()
+            want = oracle.qsa_topk(row[None, :], 1, stride, K_BLK, RATIO, pos, WIDTH)[0]
+            got = rt.download(d_sel, WIDTH * 4, np.int32)
+            assert np.array_equal(got, want), (pos, np.flatnonzero(got != want)[:8])
+            epos = pos // 2 + 40000
+            lib.q4_hip_pos_push(epos)
+            assert lib.q4_hip_qsa_topk_d(d_o, d_osel, stride, K_BLK, RATIO, WIDTH)
+            rt.sync()
+            want = oracle.qsa_topk(other[None, :], 1, stride, K_BLK, RATIO, epos, WIDTH)[0]
+            got = rt.download(d_osel, WIDTH * 4, np.int32)
+            assert np.array_equal(got, want), ("eager", epos, np.flatnonzero(got != want)[:8])
+    finally:
+        lib.q4_hip_graph_free(g)
+    for p_ in (d_sc, d_sel, d_o, d_osel):
+        rt.free(p_)
+
+
 def test_topk_rows_bit_exact(rt, oracle):
     """Prefill form: n_tok rows, one per token at pos0 + t, crossing the
     dense-prefix boundary, with small k_blk and width."""
