@@ -113,6 +113,27 @@ def test_topk_d_split_row_graph_replays(rt, oracle):
         rt.free(p_)
 
 
+@pytest.mark.parametrize("k_blk,width", [(1, 16), (37, 300), (511, WIDTH)])
+def test_topk_d_split_row_small_k(rt, oracle, k_blk, width):
+    """The split selection (a row capacity of 16385-65536 blocks) at other
+    k_blk and widths: lists shorter than the width take the tail rule, and
+    each slice's local candidate bin follows its own need."""
+    lib = rt.lib
+    rng = np.random.default_rng(4300 + k_blk)
+    stride, pos = 60000, 200001
+    for name, row in _score_rows(rng, stride):
+        note(f"split topk_d k_blk={k_blk} width={width} rows={name}")
+        d_sc, d_sel = rt.upload(row[None, :]), rt.alloc(width * 4)
+        lib.q4_hip_pos_push(pos)
+        assert lib.q4_hip_qsa_topk_d(d_sc, d_sel, stride, k_blk, RATIO, width)
+        rt.sync()
+        got = rt.download(d_sel, width * 4, np.int32)
+        want = oracle.qsa_topk(row[None, :], 1, stride, k_blk, RATIO, pos, width)[0]
+        rt.free(d_sc)
+        rt.free(d_sel)
+        assert np.array_equal(got, want), (k_blk, name, np.flatnonzero(got != want)[:8])
+
+
 def test_topk_rows_bit_exact(rt, oracle):
     """Prefill form: n_tok rows, one per token at pos0 + t, crossing the
     dense-prefix boundary, with small k_blk and width."""
