@@ -632,7 +632,7 @@ template <uint32_t KPT> struct TopkShape {
 };
 
 /* Split selection of one device-position row of up to 65536 keys: workgroup
- * w of G reduces keys w*4096 .. +4095 to its local candidates (its keys
+ * w of G reduces keys w*8192 .. +8191 (TK_T * TKS_KPS) to its local candidates (its keys
  * within the distance bin where its own count reaches need: every key of
  * the row's top need is among them, since such a key has fewer than need
  * greater keys in the row, so in its slice), in index order, plus its
