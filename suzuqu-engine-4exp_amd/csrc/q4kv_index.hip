@@ -521,10 +521,10 @@ template <uint32_t HC, uint32_t CAP> union TopkHist {
     uint32_t dist[TK_DBINS * HC];    /* distance bins x HC copies */
     uint32_t cand[1u << TK_CBITS];   /* candidate passes */
 };
-template <uint32_t HC, uint32_t CAP> struct TopkSmem {
+template <uint32_t HC, uint32_t CAP, uint32_t NT> struct TopkSmem {
     TopkHist<HC, CAP> h;
-    uint32_t cg[TK_T], ce[TK_T];     /* per (key row, wave) counts -> offsets */
-    uint64_t wm[TK_T];               /* per (key row, wave) candidate lane masks */
+    uint32_t cg[NT], ce[NT];         /* per (key row, wave) counts -> offsets */
+    uint64_t wm[NT];                 /* per (key row, wave) candidate lane masks */
     uint32_t ckey[CAP];              /* candidates in index order */
     int32_t cidx[CAP];
     uint32_t bins[TK_DBINS];
@@ -552,8 +552,9 @@ __device__ inline uint32_t wave_max_u32(uint32_t x) {
     x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
     return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
 }
-/* Exclusive prefix sum over the 1024 threads in thread order; *total gets
- * the sum. Uses wtot[0]; ends with a barrier so wtot may be reused. */
+/* Exclusive prefix sum over the NW waves' threads in thread order; *total
+ * gets the sum. Uses wtot[0]; ends with a barrier so wtot may be reused. */
+template <uint32_t NW = 16>
 __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t *wtot, uint32_t *total) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t inc = wave_incl_scan(v);
@@ -561,7 +562,7 @@ __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t *wtot, uint32_t 
     __syncthreads();
     uint32_t pre = 0, tot = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < 16; w++) {
+    for (uint32_t w = 0; w < NW; w++) {
         const uint32_t x = wtot[w];
         pre += w < wave ? x : 0u;
         tot += x;
@@ -573,6 +574,7 @@ __device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t *wtot, uint32_t 
 
 /* The same without the trailing barrier: the caller separates two uses of
  * one wtot buffer by another barrier. Returns the exclusive prefix. */
+template <uint32_t NW = 16>
 __device__ inline uint32_t block_excl_scan_nb(uint32_t v, uint32_t *wtot) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t inc = wave_incl_scan(v);
@@ -580,7 +582,7 @@ __device__ inline uint32_t block_excl_scan_nb(uint32_t v, uint32_t *wtot) {
     __syncthreads();
     uint32_t pre = 0;
 #pragma unroll
-    for (uint32_t w = 0; w < 16; w++) pre += w < wave ? wtot[w] : 0u;
+    for (uint32_t w = 0; w < NW; w++) pre += w < wave ? wtot[w] : 0u;
     return pre + inc - v;
 }
 
@@ -625,10 +627,11 @@ enum { TK_ROWS = 0, TK_DEV = 1, TK_BATCH = 2 };
  * histogram copies and 2048 candidates, so that two workgroups share a CU
  * (with 8 copies the histogram's bank conflicts cost the prefill indexer
  * 1.2 %). */
-template <uint32_t KPT> struct TopkShape {
-    static constexpr uint32_t HC = KPT <= 8u ? 16u : 32u;
-    static constexpr uint32_t CAP = KPT <= 8u ? 2048u : TK_CAP;
-    static constexpr int WG_PER_CU = KPT <= 8u ? 2 : 1;
+template <uint32_t KPT, uint32_t NT = TK_T> struct TopkShape {
+    static constexpr bool SMALL = KPT * NT <= 8192u; /* rows of up to 8192 blocks */
+    static constexpr uint32_t HC = SMALL ? 16u : 32u;
+    static constexpr uint32_t CAP = SMALL ? 2048u : TK_CAP;
+    static constexpr int WG_PER_CU = SMALL ? 2 : 1; /* LDS allows two */
 };
 
 /* Split selection of one device-position row of up to 65536 keys: workgroup
@@ -662,15 +665,17 @@ __device__ inline uint32_t ld_agent(const uint32_t *p) {
 constexpr int TKS_SC1 = 16; /* buffer-load cache policy: sc1 */
 __device__ TopkSplitScratch tks_scratch;
 
-template <int SRC, uint32_t KPT, uint32_t SPLIT = 0>
-__global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(const float *score, int32_t *sel,
+template <int SRC, uint32_t KPT, uint32_t SPLIT = 0, uint32_t NT = TK_T>
+__global__ __launch_bounds__(NT, (TopkShape<KPT, NT>::WG_PER_CU)) void qsa_topk_k(const float *score, int32_t *sel,
                                                    uint32_t stride, uint32_t k_blk,
                                                    uint32_t ratio, uint32_t pos0,
                                                    uint32_t width, const int32_t *pp,
                                                    const q4kv_index_desc *descs) {
-    constexpr uint32_t HC = TopkShape<KPT>::HC, CAP = TopkShape<KPT>::CAP;
-    __shared__ TopkSmem<HC, CAP> sm;
-    static_assert(!SPLIT || SRC == TK_DEV, "split rows are device-position rows");
+    constexpr uint32_t HC = TopkShape<KPT, NT>::HC, CAP = TopkShape<KPT, NT>::CAP;
+    constexpr uint32_t NW = NT / 64u; /* waves */
+    __shared__ TopkSmem<HC, CAP, NT> sm;
+    static_assert(!SPLIT || (SRC == TK_DEV && NT == TK_T), "split rows: device-position, 1024 threads");
+    static_assert(NT >= 256u && NT <= TK_T && KPT * NW <= NT && CAP % NT == 0u, "row layout");
     /* t: the row (token or batch item); with SPLIT the slice of the one row */
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     const uint32_t lane = tid & 63u, wave = tid >> 6;
@@ -692,10 +697,10 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
     const uint32_t need = n_vis < k_blk ? n_vis : k_blk;
     if (need == n_vis) { /* every complete block fits: the dense prefix */
         if (SPLIT && t != 0) return;
-        for (uint32_t w = tid; w < width; w += TK_T) stg(out + w, w <= pos ? (int32_t)w : -1);
+        for (uint32_t w = tid; w < width; w += NT) stg(out + w, w <= pos ? (int32_t)w : -1);
         return;
     }
-    constexpr uint32_t TK_CHUNK = TK_T * KPT;
+    constexpr uint32_t TK_CHUNK = NT * KPT;
     const uint32_t nchunk = (n_vis + TK_CHUNK - 1) / TK_CHUNK;
     uint32_t key[KPT];
     /* Elements past n_vis get key 0, the smallest key. Since need <= n_vis
@@ -707,7 +712,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         const uint32_t lim = n_vis - c * TK_CHUNK;
         if (lim >= TK_CHUNK) {
 #pragma unroll
-            for (uint32_t r = 0; r < KPT; r++) key[r] = xkey(ldg(src + r * TK_T + tid));
+            for (uint32_t r = 0; r < KPT; r++) key[r] = xkey(ldg(src + r * NT + tid));
         } else {
             /* a partial chunk through a buffer resource of lim elements:
              * loads past it return 0 with no branch, so all KPT loads are in
@@ -718,33 +723,33 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
 #pragma unroll
             for (uint32_t r = 0; r < KPT; r++)
                 key[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(tid * 4u),
-                                                              (int)(r * TK_T * 4u), 0);
+                                                              (int)(r * NT * 4u), 0);
 #pragma unroll
             for (uint32_t r = 0; r < KPT; r++) {
                 /* xkey with its sign-bit term only where the element is in
                  * the row: past it the word loaded is 0 and its key then 0,
                  * with no select (which would move the load under it) */
                 const uint32_t u = key[r];
-                const uint32_t in = (r * TK_T + tid - lim) & 0x80000000u;
+                const uint32_t in = (r * NT + tid - lim) & 0x80000000u;
                 key[r] = u ^ ((uint32_t)((int32_t)u >> 31) | in);
             }
         }
     };
-    auto valid = [&](uint32_t c, uint32_t r) { return c * TK_CHUNK + r * TK_T + tid < n_vis; };
+    auto valid = [&](uint32_t c, uint32_t r) { return c * TK_CHUNK + r * NT + tid < n_vis; };
 
     bool fast = nchunk == 1;
     uint32_t above = 0, ncand = 0, Kc = 0;
     if constexpr (SPLIT != 0) {
         /* ---- this workgroup's slice (SK keys, SPLIT per thread): keys,
          * maximum, distance histogram ---- */
-        constexpr uint32_t KS = SPLIT, SK = TK_T * KS;
-        constexpr uint32_t GMAX = TK_CHUNK / SK, P = (TK_T / 64u) / GMAX; /* waves per slice */
+        constexpr uint32_t KS = SPLIT, SK = NT * KS;
+        constexpr uint32_t GMAX = TK_CHUNK / SK, P = (NT / 64u) / GMAX; /* waves per slice */
         static_assert(GMAX <= TKS_G && P >= 1u, "slices fit the scratch and the waves");
         constexpr uint32_t LR = TKS_CAPW / P, LK = LR / 64u; /* list entries per wave, per lane */
         const uint32_t G = gridDim.x, base = t * SK;
         const uint32_t lim = n_vis > base ? min(n_vis - base, SK) : 0u;
         TopkSplitScratch &gs = tks_scratch;
-        for (uint32_t i = tid; i < TK_DBINS * TKS_HC; i += TK_T) sm.h.dist[i] = 0;
+        for (uint32_t i = tid; i < TK_DBINS * TKS_HC; i += NT) sm.h.dist[i] = 0;
         uint32_t ks[KS];
         {
             /* loads past the slice's visible keys return 0 (buffer bound),
@@ -754,11 +759,11 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
 #pragma unroll
             for (uint32_t r = 0; r < KS; r++)
                 ks[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(tid * 4u),
-                                                             (int)(r * TK_T * 4u), 0);
+                                                             (int)(r * NT * 4u), 0);
 #pragma unroll
             for (uint32_t r = 0; r < KS; r++) {
                 const uint32_t u = ks[r];
-                const uint32_t in = (r * TK_T + tid - lim) & 0x80000000u;
+                const uint32_t in = (r * NT + tid - lim) & 0x80000000u;
                 ks[r] = u ^ ((uint32_t)((int32_t)u >> 31) | in);
             }
         }
@@ -770,13 +775,13 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         __syncthreads();
         uint32_t M = 0;
 #pragma unroll
-        for (uint32_t w = 0; w < 16; w++) M = max(M, sm.wtot[1][w]);
+        for (uint32_t w = 0; w < NW; w++) M = max(M, sm.wtot[1][w]);
         const uint32_t Mb = M >> TK_DSHIFT;
         uint32_t dist[KS];
 #pragma unroll
         for (uint32_t r = 0; r < KS; r++) {
             dist[r] = min(Mb - (ks[r] >> TK_DSHIFT), TK_DBINS - 1u);
-            if (r * TK_T + tid < lim)
+            if (r * NT + tid < lim)
                 atomicAdd(sm.h.dist + (lane & (TKS_HC - 1u)) + dist[r] * TKS_HC, 1u);
         }
         __syncthreads();
@@ -808,7 +813,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         uint64_t cm[KS];
 #pragma unroll
         for (uint32_t r = 0; r < KS; r++) {
-            cm[r] = __ballot((r * TK_T + tid < lim) & (dist[r] <= Bw));
+            cm[r] = __ballot((r * NT + tid < lim) & (dist[r] <= Bw));
             if (lane == 0) sm.cg[r * 16u + wave] = (uint32_t)__popcll(cm[r]);
         }
         __syncthreads();
@@ -831,7 +836,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                 if ((cm[r] >> lane) & 1u) {
                     const uint32_t i = sm.ce[r * 16u + wave] + lanes_below(cm[r]);
                     st_agent(&gs.key[t][i], ks[r]);
-                    st_agent(&gs.idx[t][i], base + r * TK_T + tid);
+                    st_agent(&gs.idx[t][i], base + r * NT + tid);
                 }
             }
         }
@@ -891,7 +896,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
             sm.ce[tid] = cntv;
         }
         if (tid < TK_DBINS) sm.bins[tid] = 0;
-        for (uint32_t i = tid; i < (1u << TK_CBITS); i += TK_T) sm.h.cand[i] = 0;
+        for (uint32_t i = tid; i < (1u << TK_CBITS); i += NT) sm.h.cand[i] = 0;
         if (tid == 0) sm.st[0] = TK_DBINS - 1u;
         __syncthreads();
         uint32_t Mg = 0;
@@ -963,7 +968,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
             __syncthreads();
         }
     } else if (fast) {
-        for (uint32_t i = tid; i < TK_DBINS * HC; i += TK_T) sm.h.dist[i] = 0;
+        for (uint32_t i = tid; i < TK_DBINS * HC; i += NT) sm.h.dist[i] = 0;
         sm.wm[tid] = 0;
         load_chunk(0);
         /* ---- row maximum (as the loads land) ---- */
@@ -975,7 +980,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         __syncthreads();
         uint32_t M = 0;
 #pragma unroll
-        for (uint32_t w = 0; w < 16; w++) M = max(M, sm.wtot[1][w]);
+        for (uint32_t w = 0; w < NW; w++) M = max(M, sm.wtot[1][w]);
         /* ---- histogram of the distance from the maximum in 1/16-octave
          * steps of |score| (the keys' bits above bit 19), clamped at 511;
          * 32 copies keep a half-wave's atomics on distinct banks ---- */
@@ -985,15 +990,26 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         for (uint32_t r = 0; r < KPT; r++)
             atomicAdd(hc + min(Mb - (key[r] >> TK_DSHIFT), TK_DBINS - 1u) * HC, 1u);
         __syncthreads();
-        { /* fold the copies: two threads per bin, each reading its half in an
-           * order rotated by the bin, so a wave's reads spread over the banks
-           * (in order, lanes 16 dwords apart would meet 16 to a bank) */
+        if constexpr (NT == TK_T) {
+            /* fold the copies: two threads per bin, each reading its half in
+             * an order rotated by the bin, so a wave's reads spread over the
+             * banks (in order, lanes 16 dwords apart would meet 16 to a bank) */
             const uint32_t *hp = sm.h.dist + (tid >> 1) * HC + (tid & 1u) * (HC / 2u);
             uint32_t v = 0;
 #pragma unroll
             for (uint32_t i = 0; i < HC / 2u; i++) v += hp[(i + (tid >> 1)) & (HC / 2u - 1u)];
             v += __shfl_xor(v, 1);
             if ((tid & 1u) == 0) sm.bins[tid >> 1] = v;
+        } else {
+            /* TK_DBINS / NT bins per thread, all copies, rotated by the bin */
+#pragma unroll
+            for (uint32_t b = tid; b < TK_DBINS; b += NT) {
+                const uint32_t *hp = sm.h.dist + b * HC;
+                uint32_t v = 0;
+#pragma unroll
+                for (uint32_t i = 0; i < HC; i++) v += hp[(i + b) & (HC - 1u)];
+                sm.bins[b] = v;
+            }
         }
         __syncthreads();
         if (wave == 0) { /* the nearest bin where the count reaches need */
@@ -1030,19 +1046,19 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
             for (uint32_t r = 32; r < KPT; r++) mhi |= key[r] >= Kc ? 1u << (r - 32) : 0u;
             const uint64_t mine0 = ((uint64_t)mhi << 32) | mlo;
             for (uint64_t m = mine0; m; m &= m - 1ull)
-                atomicOr(&sm.wm[(uint32_t)__builtin_ctzll(m) * 16u + wave], 1ull << lane);
+                atomicOr(&sm.wm[(uint32_t)__builtin_ctzll(m) * NW + wave], 1ull << lane);
             __syncthreads();
             uint32_t tot;
-            const uint32_t off = block_excl_scan((uint32_t)__popcll(sm.wm[tid]), sm.wtot[0], &tot);
+            const uint32_t off = block_excl_scan<NW>((uint32_t)__popcll(sm.wm[tid]), sm.wtot[0], &tot);
             sm.cg[tid] = off;
-            for (uint32_t i = tid; i < (1u << TK_CBITS); i += TK_T) sm.h.cand[i] = 0;
+            for (uint32_t i = tid; i < (1u << TK_CBITS); i += NT) sm.h.cand[i] = 0;
             __syncthreads();
             const uint64_t below = (1ull << lane) - 1ull;
             for (uint64_t m = mine0; m; m &= m - 1ull) {
                 const uint32_t r = (uint32_t)__builtin_ctzll(m);
-                const uint32_t j = r * 16u + wave;
+                const uint32_t j = r * NW + wave;
                 const uint32_t i = sm.cg[j] + (uint32_t)__popcll(sm.wm[j] & below);
-                const uint32_t e = r * TK_T + tid;
+                const uint32_t e = r * NT + tid;
                 sm.ckey[i] = xkey(ldg(row + e));
                 sm.cidx[i] = (int32_t)e;
             }
@@ -1057,24 +1073,38 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         for (uint32_t pass = 0; pass < 2; pass++) {
             const uint32_t lo = pass == 0 ? 9u : 0u, wbits = pass == 0 ? 10u : 9u;
             const uint32_t nd = 1u << wbits;
-            for (uint32_t i = tid; i < ncand; i += TK_T) {
+            for (uint32_t i = tid; i < ncand; i += NT) {
                 const uint32_t u = sm.ckey[i];
                 const uint32_t v = u & ((1u << TK_DSHIFT) - 1u);
                 if ((u >> TK_DSHIFT) == kb && (pass == 0 || (v >> 9) == pre))
                     atomicAdd(&sm.h.cand[(v >> lo) & (nd - 1u)], 1u);
             }
             __syncthreads();
-            /* thread t owns digit nd-1-t (descending) */
-            const int d = (int)nd - 1 - (int)tid;
-            const uint32_t c = d >= 0 ? sm.h.cand[d] : 0u;
-            const uint32_t acc = block_excl_scan_nb(c, sm.wtot[pass]);
+            /* thread t owns digits nd-1-DPT*t .. (descending), DPT of them */
+            constexpr uint32_t DPT = (1u << TK_CBITS) / NT;
+            uint32_t c[DPT], cs = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < DPT; j++) {
+                const int d = (int)nd - 1 - (int)(DPT * tid + j);
+                c[j] = d >= 0 ? sm.h.cand[d] : 0u;
+                cs += c[j];
+            }
+            uint32_t acc = block_excl_scan_nb<NW>(cs, sm.wtot[pass]);
             const uint32_t target = need - gt;
-            if (acc < target && acc + c >= target) {
-                sm.st[4 + 2 * pass] = (uint32_t)d;
-                sm.st[5 + 2 * pass] = acc;
+#pragma unroll
+            for (uint32_t j = 0; j < DPT; j++) {
+                if (acc < target && acc + c[j] >= target) {
+                    sm.st[4 + 2 * pass] = nd - 1u - (DPT * tid + j);
+                    sm.st[5 + 2 * pass] = acc;
+                }
+                acc += c[j];
             }
             __syncthreads();
-            if (d >= 0) sm.h.cand[d] = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < DPT; j++) {
+                const int d = (int)nd - 1 - (int)(DPT * tid + j);
+                if (d >= 0) sm.h.cand[d] = 0;
+            }
             pre = pass == 0 ? sm.st[4] : (pre << 9) | sm.st[6];
             gt += sm.st[5 + 2 * pass];
             __syncthreads();
@@ -1082,20 +1112,21 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         const uint32_t thr = Kc | pre;
         const uint32_t n_gt = gt, rem = need - n_gt;
         /* ---- ordered output over the index-ordered candidates ---- */
+        constexpr uint32_t CPT = CAP / NT; /* candidates per thread */
         uint32_t g = 0, e = 0;
-        const uint32_t i0 = 4u * tid;
+        const uint32_t i0 = CPT * tid;
 #pragma unroll
-        for (uint32_t j = 0; j < 4; j++) {
+        for (uint32_t j = 0; j < CPT; j++) {
             const uint32_t i = i0 + j;
             if (i < ncand) {
                 g += sm.ckey[i] > thr;
                 e += sm.ckey[i] == thr;
             }
         }
-        const uint32_t pk = block_excl_scan_nb(g | (e << 16), sm.wtot[2]);
+        const uint32_t pk = block_excl_scan_nb<NW>(g | (e << 16), sm.wtot[2]);
         uint32_t og = pk & 0xffffu, oe = pk >> 16;
 #pragma unroll
-        for (uint32_t j = 0; j < 4; j++) {
+        for (uint32_t j = 0; j < CPT; j++) {
             const uint32_t i = i0 + j;
             if (i < ncand) {
                 const uint32_t u = sm.ckey[i];
@@ -1115,7 +1146,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
         if (SPLIT && nchunk == 1) load_chunk(0);
         if (tid == 0) { sm.st[4] = 0; sm.st[5] = 0; }
         for (uint32_t pass = 0; pass < 4; pass++) {
-            for (uint32_t i = tid; i < 256 * HC; i += TK_T) sm.h.rep[i] = 0;
+            for (uint32_t i = tid; i < 256 * HC; i += NT) sm.h.rep[i] = 0;
             __syncthreads();
             const uint32_t sh = 24u - 8u * pass;
             const uint32_t pre = sm.st[4];
@@ -1131,15 +1162,17 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                 }
             }
             __syncthreads();
-            { /* fold the copies: four lanes per bin, HC / 4 copies each, read
-               * in an order rotated by the bin (bank spread, as above) */
-                const uint32_t bin = tid >> 2, part = tid & 3u;
-                const uint32_t *hp = sm.h.rep + bin * HC + part * (HC / 4u);
+            { /* fold the copies: TPB = NT / 256 lanes per bin, HC / TPB copies
+               * each, read in an order rotated by the bin (bank spread, as
+               * above) */
+                constexpr uint32_t TPB = NT / 256u;
+                const uint32_t bin = tid / TPB, part = tid % TPB;
+                const uint32_t *hp = sm.h.rep + bin * HC + part * (HC / TPB);
                 uint32_t v = 0;
 #pragma unroll
-                for (uint32_t i = 0; i < HC / 4u; i++) v += hp[(i + bin) & (HC / 4u - 1u)];
-                v += __shfl_xor(v, 1);
-                v += __shfl_xor(v, 2);
+                for (uint32_t i = 0; i < HC / TPB; i++) v += hp[(i + bin) & (HC / TPB - 1u)];
+                if (TPB > 1u) v += __shfl_xor(v, 1);
+                if (TPB > 2u) v += __shfl_xor(v, 2);
                 if (part == 0) sm.bins[bin] = v;
             }
             __syncthreads();
@@ -1177,16 +1210,16 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                 gv = set_lane<r>(gv, ng);
                 ev = set_lane<r>(ev, ne);
             });
-            sm.cg[lane * 16u + wave] = gv;
-            sm.ce[lane * 16u + wave] = ev;
+            sm.cg[lane * NW + wave] = gv;
+            sm.ce[lane * NW + wave] = ev;
             __syncthreads();
             uint32_t tg, te;
-            const uint32_t og = block_excl_scan(sm.cg[tid], sm.wtot[0], &tg);
-            const uint32_t oe = block_excl_scan(sm.ce[tid], sm.wtot[1], &te);
+            const uint32_t og = block_excl_scan<NW>(sm.cg[tid], sm.wtot[0], &tg);
+            const uint32_t oe = block_excl_scan<NW>(sm.ce[tid], sm.wtot[1], &te);
             sm.cg[tid] = og;
             sm.ce[tid] = oe;
             __syncthreads();
-            const uint32_t gov = sm.cg[lane * 16u + wave], eov = sm.ce[lane * 16u + wave];
+            const uint32_t gov = sm.cg[lane * NW + wave], eov = sm.ce[lane * NW + wave];
             uint32_t thr2 = thr;
             asm volatile("" : "+v"(thr2)); /* do not carry the first loop's masks */
 #pragma unroll
@@ -1194,7 +1227,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
                 const bool gt = key[r] > thr2;
                 const bool eq = (key[r] == thr2) & ((thr2 != 0u) | valid(c, r));
                 const uint64_t bg = __ballot(gt), be = __ballot(eq);
-                const uint32_t e = c * TK_CHUNK + r * TK_T + tid;
+                const uint32_t e = c * TK_CHUNK + r * NT + tid;
                 if (bg) {
                     const uint32_t k = carry_g +
                                        (uint32_t)__builtin_amdgcn_readlane((int)gov, (int)r) +
@@ -1215,7 +1248,7 @@ __global__ __launch_bounds__(1024, TopkShape<KPT>::WG_PER_CU) void qsa_topk_k(co
     }
     /* expansion (src/q4_rocm.cu:7668-7696, 7830-7845) */
     const uint32_t ncs = need * ratio;
-    for (uint32_t w = tid; w < width; w += TK_T) {
+    for (uint32_t w = tid; w < width; w += NT) {
         int32_t v;
         if (w < ncs) {
             const uint32_t i = w / ratio, j = w - i * ratio;
@@ -1426,6 +1459,17 @@ extern "C" bool q4_hip_qsa_score_d(const float *q, const float *pool, float *sco
     return q4kv_launch_ok("qsa_score_d");
 }
 
+/* Q4KV_TOPK_NT=1024 keeps token rows of up to 8192 blocks on 1024-thread
+ * workgroups (8 keys per thread) instead of 512 (16 keys per thread). */
+static bool topk_rows_512(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("Q4KV_TOPK_NT");
+        v = (e && atoi(e) == 1024) ? 0 : 1;
+    }
+    return v != 0;
+}
+
 extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok,
                                 uint32_t n_blocks, uint32_t stride, uint32_t k_blk,
                                 uint32_t ratio, uint32_t pos0, uint32_t width) {
@@ -1437,7 +1481,12 @@ extern "C" bool q4_hip_qsa_topk(const float *score, int32_t *sel, uint32_t n_tok
     (void)hipGetLastError();
     /* the longest row decides the register layout */
     const uint64_t vis_max = ((uint64_t)pos0 + n_tok) / ratio;
-    if (vis_max <= 8u * TK_T)
+    /* rows of up to 8192 blocks (prefill slices): 512 threads per row, so
+     * the slice's rows launch half the waves */
+    if (vis_max <= 8u * TK_T && topk_rows_512())
+        qsa_topk_k<TK_ROWS, 16, 0, 512><<<n_tok, 512, 0, q4kv_stream>>>(
+            score, sel, stride, k_blk, ratio, pos0, width, nullptr, nullptr);
+    else if (vis_max <= 8u * TK_T)
         qsa_topk_k<TK_ROWS, 8><<<n_tok, TK_T, 0, q4kv_stream>>>(score, sel, stride, k_blk,
                                                                  ratio, pos0, width, nullptr,
                                                                  nullptr);
