@@ -141,6 +141,7 @@ def test_topk_rows_bit_exact(rt, oracle):
     for pos0, n_tok, k_blk, width, stride in [(2040, 20, K_BLK, WIDTH, 600),
                                               (9000, 33, 100, 300, 2300),
                                               (9000, 33, 100, 300, 8192),
+                                              (40000, 9, K_BLK, WIDTH, 12000),
                                               (70000, 6, K_BLK, WIDTH, 17503)]:
         note(f"topk rows pos0={pos0} n_tok={n_tok} k_blk={k_blk}")
         rng = np.random.default_rng(pos0)
