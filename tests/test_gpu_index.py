@@ -294,7 +294,9 @@ def test_pool_d_and_f16_store_follow_device_position(rt, oracle):
 @pytest.mark.parametrize("hd,n_rot,n_head,n_tok,pos0", [(256, 64, 16, 1, 262143),
                                                         (128, 64, 4, 9, 100000),
                                                         (256, 256, 2, 3, 5),
-                                                        (640, 32, 3, 2, 77)])
+                                                        (640, 32, 3, 2, 77),
+                                                        (128, 64, 4, 515, 20000),
+                                                        (640, 32, 3, 400, 77)])
 def test_q_k_prep_match_oracle(rt, oracle, hd, n_rot, n_head, n_tok, pos0):
     lib = rt.lib
     note(f"prep hd={hd} n_rot={n_rot} n_head={n_head} n_tok={n_tok} pos0={pos0}")
