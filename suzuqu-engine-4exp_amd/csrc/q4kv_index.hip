@@ -33,7 +33,11 @@
  *          threshold bin's candidates only. Rows that do not reduce (heavy ties,
  *          more than 65536 blocks) take four 8-bit radix passes over every
  *          key. One launch replaces the reference's ten on the
- *          device-position path.
+ *          device-position path. A device-position row of 16385-65536
+ *          blocks is split over 8 workgroups of 8192 keys that hand their
+ *          local candidates to the last one to finish; token rows of up to
+ *          8192 blocks run on 512 threads (16 keys each), which halves the
+ *          waves a prefill slice launches.
  */
 #include "q4kv_internal.h"
 #include "q4kv.h"
