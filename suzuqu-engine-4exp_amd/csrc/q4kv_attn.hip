@@ -358,7 +358,11 @@ __device__ static inline void dma16(const void *src, void *lds_wave_base) {
 /* 16 bytes global -> LDS like dma16, issued from inline assembly so that the
  * compiler does not add its own wait for the DMA before every LDS read of
  * the staging buffers (it cannot tell the two buffers apart); the kernels
- * that use it wait for their DMAs themselves, with explicit vmcnt counts. */
+ * that use it wait for their DMAs themselves, with explicit vmcnt counts.
+ * m0 is a reserved register, so its clobber is not honoured (the compiler
+ * warns): the kernels that use this issue every DMA through it and hold
+ * nothing of their own in m0 (checked in their gfx950 assembly: every m0
+ * write there is this s_mov_b32). */
 __device__ static inline void dma16_manual(const void *src, void *lds_wave_base) {
     const uint32_t m0 =
         __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(LOCAL void *)lds_wave_base);
